@@ -1,0 +1,127 @@
+/*
+ * libpiton_mi355x.so: hand-written gfx950 (MI355X, CDNA4) kernels for PIton's data-parallel
+ * kernel set, behind a plain C ABI.
+ *
+ * Conventions (every entry point):
+ *   - pointers are device pointers owned by the caller; sizes and strides are int64 element
+ *     counts; `stream` is a hipStream_t (NULL = the default stream);
+ *   - launches are asynchronous on `stream`; nothing is allocated by the library;
+ *   - arguments are validated before any HIP call; the return value is a status code below,
+ *     and piton_mi355x_last_error() gives this thread's message for the last failure.
+ *
+ * Each kernel entry replaces one `kernel[grid](...)` launch of the reference
+ * (piton/runtime/launcher.py:270-292, the `device == "emu"` / `"pi"` dispatch at :285-291),
+ * with the reference kernel's runtime arguments in the same order and meaning.
+ */
+#ifndef PITON_MI355X_H
+#define PITON_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PITON_MI355X_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define PITON_API __attribute__((visibility("default")))
+#else
+#define PITON_API
+#endif
+
+enum {
+    PITON_OK = 0,
+    PITON_EINVAL = -1,      /* invalid argument (null pointer, negative size, bad flag) */
+    PITON_EUNSUPPORTED = -2, /* valid but unsupported shape or layout */
+    PITON_EHIP = -3,        /* a HIP call failed; the message names it */
+    PITON_ENODEV = -4       /* no usable gfx950 device */
+};
+
+typedef struct {
+    int32_t cu_count;          /* compute units */
+    int32_t max_clock_khz;     /* peak engine clock */
+    int32_t mem_clock_khz;     /* memory clock */
+    int32_t mem_bus_width;     /* bits */
+    int64_t hbm_bytes;         /* device memory */
+    int32_t lds_per_cu;        /* bytes of LDS per compute unit (max per workgroup) */
+    int32_t l2_bytes;          /* L2 of one XCD as the runtime reports it */
+    int32_t wavefront_size;
+    int32_t xcd_count;         /* 0 when the runtime does not say */
+    char arch[64];             /* gcnArchName */
+} piton_device_info_t;
+
+/* Version of this ABI (PITON_MI355X_ABI_VERSION). No reference counterpart. */
+PITON_API int32_t piton_mi355x_abi_version(void);
+
+/* Message of this thread's last failed call ("" if none). No reference counterpart. */
+PITON_API const char *piton_mi355x_last_error(void);
+
+/* Properties of the current device, used for roofline figures. No reference counterpart;
+ * it plays the role of piton_qpu_count (pi/runtime/piton_rt.h:70). */
+PITON_API int32_t piton_mi355x_device_info(piton_device_info_t *out);
+
+/* matmul_kernel (examples/kernels.py:18-57): C[M,N] = A[M,K] B[K,N] in float32 through six
+ * runtime element strides; rows/cols past M/N are never stored and the K tail adds nothing.
+ * group_size_m is GROUP_SIZE_M's tile order (>= 1); it changes the order, not the bits. */
+PITON_API int32_t piton_mi355x_matmul(const float *a, const float *b, float *c, int64_t M, int64_t N,
+                            int64_t K, int64_t stride_am, int64_t stride_ak, int64_t stride_bk,
+                            int64_t stride_bn, int64_t stride_cm, int64_t stride_cn,
+                            int32_t group_size_m, void *stream);
+
+/* softmax_kernel (examples/kernels.py:60-76): one row per program; the first
+ * min(block_size, n_cols) columns of each of n_rows rows are normalised and stored, other
+ * columns are untouched. block_size is the kernel's BLOCK_SIZE constexpr (>= 1). */
+PITON_API int32_t piton_mi355x_softmax(float *out, const float *in, int64_t in_row_stride,
+                             int64_t out_row_stride, int64_t n_cols, int64_t n_rows,
+                             int64_t block_size, void *stream);
+
+/* attn_fwd_kernel (examples/attention.py:67-113): Out = softmax(Q K^T sm_scale) V per head,
+ * causal or not. Q, V, Out rows are contiguous (last stride 1) with row strides stride_qm,
+ * stride_vn, stride_om; K is read through (stride_kn, stride_kk), so [N,D] and pre-transposed
+ * [D,N] storage both work; heads advance by the stride_*h arguments. head_dim in
+ * {16, 32, 64, 128}. */
+PITON_API int32_t piton_mi355x_attn_fwd(const float *q, const float *k, const float *v, float *out,
+                              float sm_scale, int64_t stride_qh, int64_t stride_qm,
+                              int64_t stride_kh, int64_t stride_kn, int64_t stride_kk,
+                              int64_t stride_vh, int64_t stride_vn, int64_t stride_oh,
+                              int64_t stride_om, int64_t n_ctx, int64_t n_heads,
+                              int32_t head_dim, int32_t causal, void *stream);
+
+/* dense_layer_kernel (examples/nn_kernels.py:23-74): Y[M,N] = [ReLU](X[M,K] W[K,N] [+ bias]),
+ * contiguous row-major. When argmax_out is not NULL, it also receives, per row, the first
+ * index of the largest of the first n_classes outputs (examples/digits_model.py:137-139),
+ * computed from the stored values. */
+PITON_API int32_t piton_mi355x_dense(const float *x, const float *w, const float *bias, float *y,
+                           int64_t M, int64_t N, int64_t K, int32_t add_bias, int32_t relu,
+                           int32_t *argmax_out, int32_t n_classes, void *stream);
+
+/* add_kernel (examples/kernels.py:6-15): out[i] = x[i] + y[i] for i < n. */
+PITON_API int32_t piton_mi355x_add(const float *x, const float *y, float *out, int64_t n, void *stream);
+
+/* layernorm_kernel (tests/test_reroll_reduce.py:199-208): over the first n elements of each
+ * of `rows` rows (row stride row_stride), (x - mean) / sqrt(var + eps) with the biased
+ * variance and no affine; elements past n are untouched. */
+PITON_API int32_t piton_mi355x_layernorm(const float *x, float *out, int64_t n, float eps, int64_t rows,
+                               int64_t row_stride, void *stream);
+
+/* Host argmax of the digits driver (examples/digits_model.py:137-139; the firmware's scan,
+ * pi/examples/digits/main.c:140-145): out[r] = first index of the largest of x[r, 0:n]
+ * (a NaN wins at its first position, as numpy's argmax). */
+PITON_API int32_t piton_mi355x_argmax_rows(const float *x, int64_t rows, int64_t ld, int64_t n,
+                                 int32_t *out, void *stream);
+
+/* Token + position embedding gather. No reference counterpart (the reference has no decoder
+ * model): out[b, t, :] = tok[ids[b, t], :] + pos[pos_offset + t, :], ids [batch, T] with
+ * row stride ids_ld; rows of out are d_model apart. Ids outside [0, vocab) are an error
+ * reported through err_flag (set to 1; the row is written as NaN). */
+PITON_API int32_t piton_mi355x_embedding(const int32_t *ids, int64_t ids_ld, const float *tok,
+                               const float *pos, float *out, int64_t batch, int64_t T,
+                               int64_t d_model, int64_t vocab, int64_t pos_offset,
+                               int32_t *err_flag, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

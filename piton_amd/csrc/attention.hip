@@ -1,0 +1,287 @@
+// Flash attention forward: attn_fwd_kernel + _attn_fwd_inner (examples/attention.py:33-113).
+//
+// Design (gfx950, fp32 MFMA v_mfma_f32_32x32x2_f32):
+//   * workgroup = 4 wavefronts = 128 query rows of one head; each wave owns 32 queries, the
+//     workgroup walks the keys in blocks of 32 staged through LDS (two buffers, prefetched
+//     into registers while the previous block is multiplied);
+//   * the score block is computed transposed, S^T = K Q^T (keys x queries), so a lane holds
+//     16 scores of ONE query (lane % 32): the row max and row sum are 15 in-lane operations
+//     plus one exchange with lane ^ 32, and the running max / sum / rescale factor of a query
+//     live in its own lanes;
+//   * the output is accumulated transposed too, O^T += V^T P^T: the B operand of step s is
+//     exactly the lane's own score register s (key order permuted to match the MFMA's output
+//     layout), so P never moves between lanes, and alpha rescales the lane's own accumulators;
+//   * sm_scale * log2(e) is folded into Q once, and the online softmax uses v_exp_f32 (exp2)
+//     as the reference does with tl.exp2;
+//   * causal: a workgroup loads key blocks up to its last query; a wave skips the blocks
+//     entirely past its own queries; the diagonal block is masked per element; workgroups
+//     are issued longest-first;
+//   * K is read through (stride_kn, stride_kk): float4 along d for [N, D] storage, float4 along
+//     keys for pre-transposed [D, N] storage, scalar otherwise.
+#include "common.h"
+
+namespace piton {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int ABN = 32;  // keys per block
+constexpr int ABM = 128; // queries per workgroup
+
+enum : int { K_VEC_D = 0, K_VEC_N = 1, K_SCALAR = 2 };
+
+struct AttnArgs {
+    const float *q, *k, *v;
+    float *o;
+    float scale;  // sm_scale * log2(e)
+    int64_t s_qh, s_qm, s_kh, s_kn, s_kk, s_vh, s_vn, s_oh, s_om;
+    int64_t n_ctx;
+    int head_dim;
+    int causal;
+    int v_vec;  // V rows loadable as float4
+};
+
+template <int D, int KL>
+__device__ __forceinline__ void attn_load(const AttnArgs &g, int t, const float *kb, const float *vb, int64_t key0,
+                                          float (&rk)[D / 8], float (&rv)[D / 8]) {
+    // K tile: 32 keys x D -> 8 * D / 256 = D / 8 values per thread
+    if constexpr (KL == K_VEC_D) {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+            const int idx = t + 256 * i;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
+            const int64_t n = key0 + key;
+            float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (n < g.n_ctx && 4 * dq < g.head_dim) f = *reinterpret_cast<const float4 *>(kb + n * g.s_kn + 4 * dq);
+            rk[4 * i] = f.x; rk[4 * i + 1] = f.y; rk[4 * i + 2] = f.z; rk[4 * i + 3] = f.w;
+        }
+    } else if constexpr (KL == K_VEC_N) {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+            const int idx = t + 256 * i;
+            const int d = idx / 8, kq = idx % 8;
+            const int64_t n = key0 + 4 * kq;
+            float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (n < g.n_ctx && d < g.head_dim) f = *reinterpret_cast<const float4 *>(kb + d * g.s_kk + n);
+            rk[4 * i] = f.x; rk[4 * i + 1] = f.y; rk[4 * i + 2] = f.z; rk[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < D / 8; i++) {
+            const int idx = t + 256 * i;
+            const int key = idx / D, d = idx % D;
+            const int64_t n = key0 + key;
+            rk[i] = (n < g.n_ctx && d < g.head_dim) ? kb[n * g.s_kn + d * g.s_kk] : 0.f;
+        }
+    }
+    // V tile: rows contiguous along d
+    if (g.v_vec) {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+            const int idx = t + 256 * i;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
+            const int64_t n = key0 + key;
+            float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (n < g.n_ctx && 4 * dq < g.head_dim) f = *reinterpret_cast<const float4 *>(vb + n * g.s_vn + 4 * dq);
+            rv[4 * i] = f.x; rv[4 * i + 1] = f.y; rv[4 * i + 2] = f.z; rv[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < D / 8; i++) {
+            const int idx = t + 256 * i;
+            const int key = idx / D, d = idx % D;
+            const int64_t n = key0 + key;
+            rv[i] = (n < g.n_ctx && d < g.head_dim) ? vb[n * g.s_vn + d] : 0.f;
+        }
+    }
+}
+
+template <int D, int KL>
+__device__ __forceinline__ void attn_store(const AttnArgs &g, int t, float (&Ks)[ABN][D + 1], float (&Vs)[ABN][D],
+                                           const float (&rk)[D / 8], const float (&rv)[D / 8]) {
+    if constexpr (KL == K_VEC_D) {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+            const int idx = t + 256 * i;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
+#pragma unroll
+            for (int j = 0; j < 4; j++) Ks[key][4 * dq + j] = rk[4 * i + j];
+        }
+    } else if constexpr (KL == K_VEC_N) {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+            const int idx = t + 256 * i;
+            const int d = idx / 8, kq = idx % 8;
+#pragma unroll
+            for (int j = 0; j < 4; j++) Ks[4 * kq + j][d] = rk[4 * i + j];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < D / 8; i++) {
+            const int idx = t + 256 * i;
+            Ks[idx / D][idx % D] = rk[i];
+        }
+    }
+    if (g.v_vec) {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+            const int idx = t + 256 * i;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
+            *reinterpret_cast<float4 *>(&Vs[key][4 * dq]) = make_float4(rv[4 * i], rv[4 * i + 1], rv[4 * i + 2], rv[4 * i + 3]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < D / 8; i++) {
+            const int idx = t + 256 * i;
+            Vs[idx / D][idx % D] = rv[i];
+        }
+    }
+}
+
+template <int D, int KL>
+__global__ __launch_bounds__(256) void attn_fwd_kernel_f32(AttnArgs g) {
+    __shared__ float Ks[2][ABN][D + 1];
+    __shared__ float Vs[2][ABN][D];
+
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, half = lane >> 5, l31 = lane & 31;
+    const int qb = g.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;  // longest first
+    const int64_t h = blockIdx.y;
+    const int64_t q0 = (int64_t)qb * ABM + wave * 32;  // this wave's first query
+    const int64_t qi = q0 + l31;                        // this lane's query
+
+    const float *qp = g.q + h * g.s_qh;
+    const float *kbase = g.k + h * g.s_kh;
+    const float *vbase = g.v + h * g.s_vh;
+
+    // Q'^T fragments: B[k = d][n = query] for d = 2s + half, scaled by sm_scale * log2 e
+    float qf[D / 2];
+#pragma unroll
+    for (int s = 0; s < D / 2; s++) {
+        const int d = 2 * s + half;
+        qf[s] = (qi < g.n_ctx && d < g.head_dim) ? qp[qi * g.s_qm + d] * g.scale : 0.f;
+    }
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int b = 0; b < D / 32; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[b][r] = 0.f;
+    float m_i = -INFINITY, l_i = 0.f;
+
+    const int64_t nkb_all = (g.n_ctx + ABN - 1) / ABN;
+    const int64_t nkb = g.causal ? min(nkb_all, (int64_t)(qb + 1) * (ABM / ABN)) : nkb_all;
+    const int64_t wave_last = g.causal ? (q0 + 31) / ABN : nkb_all - 1;  // last block this wave needs
+
+    float rk[D / 8], rv[D / 8];
+    attn_load<D, KL>(g, t, kbase, vbase, 0, rk, rv);
+    attn_store<D, KL>(g, t, Ks[0], Vs[0], rk, rv);
+    __syncthreads();
+
+    for (int64_t kb = 0; kb < nkb; kb++) {
+        const int cur = (int)(kb & 1);
+        const bool more = kb + 1 < nkb;
+        if (more) attn_load<D, KL>(g, t, kbase, vbase, (kb + 1) * ABN, rk, rv);
+
+        if (kb <= wave_last) {
+            // S^T block: A = K [key][d], B = Q'^T
+            f32x16 st;
+#pragma unroll
+            for (int r = 0; r < 16; r++) st[r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < D / 2; s++)
+                st = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[cur][l31][2 * s + half], qf[s], st, 0, 0, 0);
+
+            // masks: register r holds key kb*32 + 8*(r/4) + 4*half + r%4 of query qi
+            const int64_t key0 = kb * ABN + 4 * half;
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t key = key0 + 8 * (r >> 2) + (r & 3);
+                if (key >= g.n_ctx || (g.causal && key > qi)) st[r] = -INFINITY;
+                mloc = fmaxf(mloc, st[r]);
+            }
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+            const float m_new = fmaxf(m_i, mloc);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;  // rows with nothing visible yet
+            const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
+            float lsum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                st[r] = __builtin_amdgcn_exp2f(st[r] - m_use);
+                lsum += st[r];
+            }
+            lsum += __shfl_xor(lsum, 32);
+            l_i = l_i * alpha + lsum;
+            m_i = m_new;
+
+            // O^T = O^T * alpha + V^T P^T; step s pairs key (s/4)*8 + 4*half + s%4 with P^T
+            // register s of this lane
+#pragma unroll
+            for (int b = 0; b < D / 32; b++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[b][r] *= alpha;
+#pragma unroll
+                for (int s = 0; s < 16; s++) {
+                    const int key = (s >> 2) * 8 + 4 * half + (s & 3);
+                    o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[cur][key][b * 32 + l31], st[s], o[b], 0, 0, 0);
+                }
+            }
+        }
+
+        if (more) attn_store<D, KL>(g, t, Ks[cur ^ 1], Vs[cur ^ 1], rk, rv);
+        __syncthreads();
+    }
+
+    if (qi < g.n_ctx) {
+        const float inv = 1.0f / l_i;
+        float *op = g.o + h * g.s_oh + qi * g.s_om;
+#pragma unroll
+        for (int b = 0; b < D / 32; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int d = b * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (d < g.head_dim) op[d] = o[b][r] * inv;
+            }
+    }
+}
+
+template <int D>
+static void launch_d(int kl, const AttnArgs &g, dim3 grid, hipStream_t st) {
+    if (kl == K_VEC_D) hipLaunchKernelGGL((attn_fwd_kernel_f32<D, K_VEC_D>), grid, dim3(256), 0, st, g);
+    else if (kl == K_VEC_N) hipLaunchKernelGGL((attn_fwd_kernel_f32<D, K_VEC_N>), grid, dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((attn_fwd_kernel_f32<D, K_SCALAR>), grid, dim3(256), 0, st, g);
+}
+
+}  // namespace piton
+
+extern "C" int32_t piton_mi355x_attn_fwd(const float *q, const float *k, const float *v, float *out, float sm_scale,
+                                         int64_t stride_qh, int64_t stride_qm, int64_t stride_kh, int64_t stride_kn,
+                                         int64_t stride_kk, int64_t stride_vh, int64_t stride_vn, int64_t stride_oh,
+                                         int64_t stride_om, int64_t n_ctx, int64_t n_heads, int32_t head_dim,
+                                         int32_t causal, void *stream) {
+    using namespace piton;
+    PITON_REQUIRE(n_ctx >= 0 && n_heads >= 0, PITON_EINVAL, "attn_fwd: negative N_CTX or heads");
+    PITON_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, PITON_EUNSUPPORTED,
+                  "attn_fwd: HEAD_DIM %d not in {16, 32, 64, 128}", head_dim);
+    PITON_REQUIRE(n_ctx == 0 || n_heads == 0 || (q && k && v && out), PITON_EINVAL, "attn_fwd: null pointer");
+    PITON_REQUIRE(aligned4(q) && aligned4(k) && aligned4(v) && aligned4(out), PITON_EINVAL,
+                  "attn_fwd: pointers must be 4-byte aligned");
+    PITON_REQUIRE(n_heads <= 65535, PITON_EUNSUPPORTED, "attn_fwd: %lld heads exceed grid axis 1", (long long)n_heads);
+    int rc = require_device();
+    if (rc) return rc;
+    if (n_ctx == 0 || n_heads == 0) return PITON_OK;
+
+    AttnArgs g{q, k, v, out, sm_scale * 1.44269504088896341f, stride_qh, stride_qm, stride_kh, stride_kn, stride_kk,
+               stride_vh, stride_vn, stride_oh, stride_om, n_ctx, head_dim, causal ? 1 : 0, 0};
+    g.v_vec = aligned16(v) && stride_vn % 4 == 0 && stride_vh % 4 == 0 && head_dim % 4 == 0;
+    int kl = K_SCALAR;
+    if (stride_kk == 1 && stride_kn % 4 == 0 && stride_kh % 4 == 0 && aligned16(k) && head_dim % 4 == 0) kl = K_VEC_D;
+    else if (stride_kn == 1 && stride_kk % 4 == 0 && stride_kh % 4 == 0 && aligned16(k) && n_ctx % 4 == 0) kl = K_VEC_N;
+    const dim3 grid((unsigned)((n_ctx + ABM - 1) / ABM), (unsigned)n_heads);
+    hipStream_t st = (hipStream_t)stream;
+    if (head_dim <= 32) launch_d<32>(kl, g, grid, st);
+    else if (head_dim == 64) launch_d<64>(kl, g, grid, st);
+    else launch_d<128>(kl, g, grid, st);
+    rc = check_launch("attn_fwd");
+    if (rc == PITON_OK) clear_error();
+    return rc;
+}

@@ -1,0 +1,83 @@
+// Shared helpers of libpiton_mi355x.so: status codes and the thread-local error message,
+// argument checks, wavefront reductions built from DPP lane moves, and the XCD-aware
+// workgroup order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/piton_mi355x.h"
+
+namespace piton {
+
+// native 4 x float vector (the nontemporal builtins take native vector pointers)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------------------------------
+// status and messages (host)
+// ------------------------------------------------------------------------------------------
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+// PITON_OK when a gfx950 device is current, else PITON_ENODEV / PITON_EHIP with a message.
+int require_device();
+// Turns the last launch's status into PITON_OK or PITON_EHIP naming `what`.
+int check_launch(const char *what);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+#define PITON_REQUIRE(cond, code, ...)                  \
+    do {                                                \
+        if (!(cond)) return ::piton::set_error((code), __VA_ARGS__); \
+    } while (0)
+
+// ------------------------------------------------------------------------------------------
+// device helpers
+// ------------------------------------------------------------------------------------------
+
+// DPP lane move of a float within rows of 16 lanes (dpp_ctrl: quad_perm, row mirrors).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// DPP control words (GFX9 encoding).
+constexpr int DPP_QUAD_XOR1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+struct MaxOp {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct SumOp {
+    __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+
+// Reduction over one 64-lane wavefront, result in every lane: four DPP steps combine each row
+// of 16 lanes, then the four row results are read out of lanes 0, 16, 32, 48.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = op(v, dpp_f<DPP_QUAD_XOR1>(v));
+    v = op(v, dpp_f<DPP_QUAD_XOR2>(v));
+    v = op(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
+    v = op(v, dpp_f<DPP_ROW_MIRROR>(v));
+    float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return op(op(a, b), op(c, d));
+}
+
+// Workgroup order for an XCD-partitioned chip: the dispatcher hands workgroup b to XCD
+// b % n_xcd, so renumber to give each XCD a contiguous run of logical ids (neighbouring tiles
+// then share that XCD's L2). A bijection on [0, n) for any n.
+__device__ __forceinline__ int xcd_logical_id(int b, int n, int n_xcd) {
+    int q = n / n_xcd, r = n % n_xcd;
+    int x = b % n_xcd, i = b / n_xcd;
+    return x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
+constexpr int kXcdCount = 8;  // MI355X: 8 XCDs of 32 CUs
+
+}  // namespace piton

@@ -1,0 +1,364 @@
+// fp32 GEMM on CDNA4 matrix cores: matmul_kernel (examples/kernels.py:18-57) and
+// dense_layer_kernel (examples/nn_kernels.py:23-74).
+//
+// Design (gfx950):
+//   * workgroup = 256 threads = 4 wavefronts in a 2x2 grid; workgroup tile 128x128, each wave
+//     owns 64x64 = 2x2 blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per block);
+//   * K advances in tiles of 32: global -> registers (prefetch of tile k+1 while tile k is
+//     multiplied) -> LDS (two buffers, one barrier per tile) -> MFMA operands;
+//   * LDS holds A transposed (As[k][m]) and B as is (Bs[k][n]); an MFMA operand is then 32
+//     consecutive floats per half-wave (lanes 0-31 read row k, lanes 32-63 row k+1), free of
+//     bank conflicts; A's row stride is odd so the transposing writes spread over the banks;
+//   * each operand has three loaders chosen on the host: float4 along its contiguous
+//     dimension (either orientation) when the strides and base allow 16-byte loads, else
+//     scalar loads with runtime strides (the ragged / padded / odd-stride cases);
+//   * rows past M and columns past N load zeros and are never stored; the K tail loads zeros,
+//     so the stored elements equal sum_k A[m,k] B[k,n] exactly as the reference's masks give;
+//   * tile order: workgroups renumbered so each XCD gets a contiguous run of logical ids,
+//     then the reference's GROUP_SIZE_M grouping (kernels.py:28-36) on those ids.
+#include "common.h"
+
+namespace piton {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int GBM = 128, GBN = 128, GBK = 32, GTHREADS = 256;
+constexpr int kStrideAT = GBM + 1;  // As[k][m]: odd row stride for the transposing writes
+constexpr int kStrideB = GBN + 4;   // Bs[k][n]: 16-byte aligned rows for float4 writes
+constexpr int kStrideBT = GBN + 1;  // Bs[k][n] written from k-contiguous B
+
+enum : int { VEC_ROW = 0, VEC_COL = 1, SCALAR = 2 };
+
+struct GemmArgs {
+    const float *a, *b;
+    float *c;
+    int64_t M, N, K;
+    int64_t s_am, s_ak, s_bk, s_bn, s_cm, s_cn;
+    int group_m;
+    const float *bias;  // dense epilogue (nullable)
+    int relu;
+    int a_kfast, b_nfast;  // scalar loaders: which index runs fastest across threads
+};
+
+// Loads the A tile (GBM x GBK at m0, k0) into 16 registers per thread.
+// A_L == VEC_ROW: k contiguous; VEC_COL: m contiguous; SCALAR: any strides.
+template <int A_L>
+__device__ __forceinline__ void load_a(const GemmArgs &g, int t, int64_t m0, int64_t k0, float (&r)[16]) {
+    if constexpr (A_L == VEC_ROW) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int row = (t >> 3) + 32 * i, kq = t & 7;
+            int64_t m = m0 + row, k = k0 + 4 * kq;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m < g.M && k < g.K) v = *reinterpret_cast<const float4 *>(g.a + m * g.s_am + k);
+            r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
+        }
+    } else if constexpr (A_L == VEC_COL) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int kk = (t >> 5) + 8 * i, mq = t & 31;
+            int64_t m = m0 + 4 * mq, k = k0 + kk;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m < g.M && k < g.K) v = *reinterpret_cast<const float4 *>(g.a + m + k * g.s_ak);
+            r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            int idx = t + GTHREADS * i;
+            int row = g.a_kfast ? idx >> 5 : idx & 127;
+            int kk = g.a_kfast ? idx & 31 : idx >> 7;
+            int64_t m = m0 + row, k = k0 + kk;
+            r[i] = (m < g.M && k < g.K) ? g.a[m * g.s_am + k * g.s_ak] : 0.f;
+        }
+    }
+}
+
+template <int A_L>
+__device__ __forceinline__ void store_a(const GemmArgs &g, int t, float (&As)[GBK][kStrideAT], const float (&r)[16]) {
+    if constexpr (A_L == VEC_ROW) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int row = (t >> 3) + 32 * i, kq = t & 7;
+#pragma unroll
+            for (int j = 0; j < 4; j++) As[4 * kq + j][row] = r[4 * i + j];
+        }
+    } else if constexpr (A_L == VEC_COL) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int kk = (t >> 5) + 8 * i, mq = t & 31;
+#pragma unroll
+            for (int j = 0; j < 4; j++) As[kk][4 * mq + j] = r[4 * i + j];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            int idx = t + GTHREADS * i;
+            int row = g.a_kfast ? idx >> 5 : idx & 127;
+            int kk = g.a_kfast ? idx & 31 : idx >> 7;
+            As[kk][row] = r[i];
+        }
+    }
+}
+
+// B tile (GBK x GBN at k0, n0). B_L == VEC_ROW: n contiguous; VEC_COL: k contiguous.
+template <int B_L>
+__device__ __forceinline__ void load_b(const GemmArgs &g, int t, int64_t k0, int64_t n0, float (&r)[16]) {
+    if constexpr (B_L == VEC_ROW) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int kk = (t >> 5) + 8 * i, nq = t & 31;
+            int64_t k = k0 + kk, n = n0 + 4 * nq;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < g.K && n < g.N) v = *reinterpret_cast<const float4 *>(g.b + k * g.s_bk + n);
+            r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
+        }
+    } else if constexpr (B_L == VEC_COL) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int col = (t >> 3) + 32 * i, kq = t & 7;
+            int64_t k = k0 + 4 * kq, n = n0 + col;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < g.K && n < g.N) v = *reinterpret_cast<const float4 *>(g.b + k + n * g.s_bn);
+            r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            int idx = t + GTHREADS * i;
+            int col = g.b_nfast ? idx & 127 : idx >> 5;
+            int kk = g.b_nfast ? idx >> 7 : idx & 31;
+            int64_t k = k0 + kk, n = n0 + col;
+            r[i] = (k < g.K && n < g.N) ? g.b[k * g.s_bk + n * g.s_bn] : 0.f;
+        }
+    }
+}
+
+template <int B_L, int SB>
+__device__ __forceinline__ void store_b(const GemmArgs &g, int t, float (&Bs)[GBK][SB], const float (&r)[16]) {
+    if constexpr (B_L == VEC_ROW) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int kk = (t >> 5) + 8 * i, nq = t & 31;
+            *reinterpret_cast<float4 *>(&Bs[kk][4 * nq]) = make_float4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+        }
+    } else if constexpr (B_L == VEC_COL) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int col = (t >> 3) + 32 * i, kq = t & 7;
+#pragma unroll
+            for (int j = 0; j < 4; j++) Bs[4 * kq + j][col] = r[4 * i + j];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            int idx = t + GTHREADS * i;
+            int col = g.b_nfast ? idx & 127 : idx >> 5;
+            int kk = g.b_nfast ? idx >> 7 : idx & 31;
+            Bs[kk][col] = r[i];
+        }
+    }
+}
+
+template <int A_L, int B_L>
+__global__ __launch_bounds__(GTHREADS) void gemm_f32_kernel(GemmArgs g) {
+    constexpr int SB = (B_L == VEC_ROW) ? kStrideB : kStrideBT;
+    __shared__ float As[2][GBK][kStrideAT];
+    __shared__ float Bs[2][GBK][SB];
+
+    const int t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l31 = lane & 31;
+
+    // tile order: XCD-contiguous logical id, then GROUP_SIZE_M grouping (kernels.py:28-36)
+    const int num_pid_m = (int)((g.M + GBM - 1) / GBM);
+    const int num_pid_n = (int)((g.N + GBN - 1) / GBN);
+    const int pid = xcd_logical_id(blockIdx.x, gridDim.x, kXcdCount);
+    const int in_group = g.group_m * num_pid_n;
+    const int group_id = pid / in_group;
+    const int first_m = group_id * g.group_m;
+    const int gsize = min(num_pid_m - first_m, g.group_m);
+    const int pid_m = first_m + (pid % in_group) % gsize;
+    const int pid_n = (pid % in_group) / gsize;
+    const int64_t m0 = (int64_t)pid_m * GBM, n0 = (int64_t)pid_n * GBN;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    float ra[16], rb[16];
+    const int nk = (int)((g.K + GBK - 1) / GBK);
+    load_a<A_L>(g, t, m0, 0, ra);
+    load_b<B_L>(g, t, 0, n0, rb);
+    store_a<A_L>(g, t, As[0], ra);
+    store_b<B_L, SB>(g, t, Bs[0], rb);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            load_a<A_L>(g, t, m0, (int64_t)(kt + 1) * GBK, ra);
+            load_b<B_L>(g, t, (int64_t)(kt + 1) * GBK, n0, rb);
+        }
+#pragma unroll
+        for (int s = 0; s < GBK / 2; s++) {
+            const int kk = 2 * s + half;
+            const float a0 = As[cur][kk][wm * 64 + l31];
+            const float a1 = As[cur][kk][wm * 64 + 32 + l31];
+            const float b0 = Bs[cur][kk][wn * 64 + l31];
+            const float b1 = Bs[cur][kk][wn * 64 + 32 + l31];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        if (more) {
+            store_a<A_L>(g, t, As[cur ^ 1], ra);
+            store_b<B_L, SB>(g, t, Bs[cur ^ 1], rb);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: accumulator r of a 32x32 block holds row 8*(r/4) + 4*half + r%4, column l31
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++) {
+            const int64_t col = n0 + wn * 64 + nb * 32 + l31;
+            if (col >= g.N) continue;
+            const float bias = g.bias ? g.bias[col] : 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t row = m0 + wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (row < g.M) {
+                    float v = acc[mb][nb][r];
+                    if (g.bias) v += bias;
+                    if (g.relu && v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
+                    g.c[row * g.s_cm + col * g.s_cn] = v;
+                }
+            }
+        }
+}
+
+// First index of the largest of x[r, 0:n] (numpy argmax rule: the first NaN wins).
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int64_t rows, int64_t ld, int64_t n, int32_t *out) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const float *row = x + r * ld;
+    int32_t best = 0;
+    float bv = row[0];
+    if (bv == bv) {
+        for (int64_t i = 1; i < n; i++) {
+            const float v = row[i];
+            if (v != v) { best = (int32_t)i; break; }
+            if (v > bv) { bv = v; best = (int32_t)i; }
+        }
+    }
+    out[r] = best;
+}
+
+static int layout_a(const GemmArgs &g) {
+    if (g.s_ak == 1 && g.s_am % 4 == 0 && g.K % 4 == 0 && aligned16(g.a)) return VEC_ROW;
+    if (g.s_am == 1 && g.s_ak % 4 == 0 && g.M % 4 == 0 && aligned16(g.a)) return VEC_COL;
+    return SCALAR;
+}
+static int layout_b(const GemmArgs &g) {
+    if (g.s_bn == 1 && g.s_bk % 4 == 0 && g.N % 4 == 0 && aligned16(g.b)) return VEC_ROW;
+    if (g.s_bk == 1 && g.s_bn % 4 == 0 && g.K % 4 == 0 && aligned16(g.b)) return VEC_COL;
+    return SCALAR;
+}
+
+template <int A_L>
+static void launch_b(int bl, const GemmArgs &g, int nwg, hipStream_t st) {
+    if (bl == VEC_ROW) hipLaunchKernelGGL((gemm_f32_kernel<A_L, VEC_ROW>), dim3(nwg), dim3(GTHREADS), 0, st, g);
+    else if (bl == VEC_COL) hipLaunchKernelGGL((gemm_f32_kernel<A_L, VEC_COL>), dim3(nwg), dim3(GTHREADS), 0, st, g);
+    else hipLaunchKernelGGL((gemm_f32_kernel<A_L, SCALAR>), dim3(nwg), dim3(GTHREADS), 0, st, g);
+}
+
+static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
+    if (g.M == 0 || g.N == 0) return PITON_OK;
+    const int64_t tiles = ((g.M + GBM - 1) / GBM) * ((g.N + GBN - 1) / GBN);
+    PITON_REQUIRE(tiles <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "%s: %lld tiles exceed one grid", what, (long long)tiles);
+    g.a_kfast = llabs(g.s_ak) <= llabs(g.s_am);
+    g.b_nfast = llabs(g.s_bn) <= llabs(g.s_bk);
+    const int al = layout_a(g), bl = layout_b(g);
+    const int nwg = (int)tiles;
+    if (al == VEC_ROW) launch_b<VEC_ROW>(bl, g, nwg, st);
+    else if (al == VEC_COL) launch_b<VEC_COL>(bl, g, nwg, st);
+    else launch_b<SCALAR>(bl, g, nwg, st);
+    return check_launch(what);
+}
+
+}  // namespace piton
+
+extern "C" {
+
+int32_t piton_mi355x_matmul(const float *a, const float *b, float *c, int64_t M, int64_t N, int64_t K,
+                            int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                            int64_t stride_cm, int64_t stride_cn, int32_t group_size_m, void *stream) {
+    using namespace piton;
+    PITON_REQUIRE(M >= 0 && N >= 0 && K >= 0, PITON_EINVAL, "matmul: negative size M=%lld N=%lld K=%lld",
+                  (long long)M, (long long)N, (long long)K);
+    PITON_REQUIRE(group_size_m >= 1, PITON_EINVAL, "matmul: GROUP_SIZE_M must be >= 1, got %d", group_size_m);
+    PITON_REQUIRE((M == 0 || N == 0) || c != nullptr, PITON_EINVAL, "matmul: null C");
+    PITON_REQUIRE((M == 0 || N == 0 || K == 0) || (a != nullptr && b != nullptr), PITON_EINVAL, "matmul: null A or B");
+    PITON_REQUIRE(aligned4(a) && aligned4(b) && aligned4(c), PITON_EINVAL, "matmul: pointers must be 4-byte aligned");
+    int rc = require_device();
+    if (rc) return rc;
+    GemmArgs g{a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn,
+               group_size_m, nullptr, 0, 0, 0};
+    rc = launch_gemm(g, (hipStream_t)stream, "matmul");
+    if (rc == PITON_OK) clear_error();
+    return rc;
+}
+
+int32_t piton_mi355x_dense(const float *x, const float *w, const float *bias, float *y, int64_t M, int64_t N,
+                           int64_t K, int32_t add_bias, int32_t relu, int32_t *argmax_out, int32_t n_classes,
+                           void *stream) {
+    using namespace piton;
+    PITON_REQUIRE(M >= 0 && N > 0 && K > 0, PITON_EINVAL, "dense: bad size M=%lld N=%lld K=%lld",
+                  (long long)M, (long long)N, (long long)K);
+    PITON_REQUIRE(x && w && y, PITON_EINVAL, "dense: null X, W or Y");
+    PITON_REQUIRE(!add_bias || bias, PITON_EINVAL, "dense: ADD_BIAS with a null bias");
+    PITON_REQUIRE(!argmax_out || (n_classes >= 1 && n_classes <= N), PITON_EINVAL,
+                  "dense: n_classes %d outside [1, N=%lld]", n_classes, (long long)N);
+    PITON_REQUIRE(aligned4(x) && aligned4(w) && aligned4(y) && aligned4(bias), PITON_EINVAL,
+                  "dense: pointers must be 4-byte aligned");
+    int rc = require_device();
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    GemmArgs g{x, w, y, M, N, K, K, 1, N, 1, N, 1, 1, add_bias ? bias : nullptr, relu ? 1 : 0, 0, 0};
+    rc = launch_gemm(g, st, "dense");
+    if (rc) return rc;
+    if (argmax_out && M > 0) {
+        hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, st, y, M, N,
+                           (int64_t)n_classes, argmax_out);
+        rc = check_launch("dense argmax");
+        if (rc) return rc;
+    }
+    clear_error();
+    return PITON_OK;
+}
+
+int32_t piton_mi355x_argmax_rows(const float *x, int64_t rows, int64_t ld, int64_t n, int32_t *out, void *stream) {
+    using namespace piton;
+    PITON_REQUIRE(rows >= 0 && n >= 1 && ld >= n, PITON_EINVAL, "argmax_rows: rows=%lld n=%lld ld=%lld",
+                  (long long)rows, (long long)n, (long long)ld);
+    PITON_REQUIRE(rows == 0 || (x && out), PITON_EINVAL, "argmax_rows: null pointer");
+    int rc = require_device();
+    if (rc) return rc;
+    if (rows == 0) return PITON_OK;
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       x, rows, ld, n, out);
+    rc = check_launch("argmax_rows");
+    if (rc == PITON_OK) clear_error();
+    return rc;
+}
+
+}  // extern "C"

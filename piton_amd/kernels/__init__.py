@@ -1,0 +1,9 @@
+"""The kernel set, declared with the reference's signatures so that `kernel[grid](...)` calls
+written for PIton run unchanged with device="mi355x". Each kernel's work is done by the HIP
+entry its docstring names; the Python body is never executed."""
+from .attention import attn_fwd_kernel
+from .nn import dense_layer_kernel, dense_tiles
+from .tutorial import add_kernel, layernorm_kernel, matmul_kernel, softmax_kernel
+
+__all__ = ["add_kernel", "matmul_kernel", "softmax_kernel", "layernorm_kernel", "dense_layer_kernel",
+           "dense_tiles", "attn_fwd_kernel"]

@@ -1,0 +1,229 @@
+"""ctypes binding of libpiton_mi355x.so and the Python entries over it.
+
+Loading order matters on ROCm: torch is imported first, so the library's libamdhip64.so.7
+dependency resolves to the HIP runtime torch already loaded (one runtime per process, shared
+device memory and streams).
+
+Every entry takes torch tensors already on the GPU (float32 / int32), checks dtype, device
+and that the elements the kernel addresses lie inside each tensor's storage, then launches
+on torch's current stream. A missing library or a failed call raises; there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_PKG = os.path.dirname(_HERE)
+DEFAULT_LIB = os.path.join(_PKG, "lib", "libpiton_mi355x.so")
+
+ABI_VERSION = 1
+OK, EINVAL, EUNSUPPORTED, EHIP, ENODEV = 0, -1, -2, -3, -4
+
+_lock = threading.Lock()
+_lib = None
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("cu_count", ctypes.c_int32), ("max_clock_khz", ctypes.c_int32),
+                ("mem_clock_khz", ctypes.c_int32), ("mem_bus_width", ctypes.c_int32),
+                ("hbm_bytes", ctypes.c_int64), ("lds_per_cu", ctypes.c_int32),
+                ("l2_bytes", ctypes.c_int32), ("wavefront_size", ctypes.c_int32),
+                ("xcd_count", ctypes.c_int32), ("arch", ctypes.c_char * 64)]
+
+
+# entry name -> argtypes (every entry returns int32)
+SIGNATURES = {
+    "piton_mi355x_device_info": [ctypes.POINTER(DeviceInfo)],
+    "piton_mi355x_matmul": [_p, _p, _p] + [_i64] * 9 + [_i32, _p],
+    "piton_mi355x_softmax": [_p, _p] + [_i64] * 5 + [_p],
+    "piton_mi355x_attn_fwd": [_p, _p, _p, _p, _f32] + [_i64] * 11 + [_i32, _i32, _p],
+    "piton_mi355x_dense": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _i32, _p],
+    "piton_mi355x_add": [_p, _p, _p, _i64, _p],
+    "piton_mi355x_layernorm": [_p, _p, _i64, _f32, _i64, _i64, _p],
+    "piton_mi355x_argmax_rows": [_p, _i64, _i64, _i64, _p, _p],
+    "piton_mi355x_embedding": [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p],
+}
+
+
+class MI355XError(RuntimeError):
+    """A failed library call: .code is the status (-1 .. -4), the message the library's."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+def library_path() -> str:
+    return os.environ.get("PITON_MI355X_LIB", DEFAULT_LIB)
+
+
+def lib():
+    """The loaded library (loaded once). Raises RuntimeError when it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = library_path()
+            if not os.path.exists(path):
+                raise RuntimeError(f"{path} is not built: run `python -m piton_amd.build` "
+                                   "(or __graft_entry__.build()) first")
+            L = ctypes.CDLL(path)
+            L.piton_mi355x_abi_version.restype = ctypes.c_int32
+            L.piton_mi355x_abi_version.argtypes = []
+            L.piton_mi355x_last_error.restype = ctypes.c_char_p
+            L.piton_mi355x_last_error.argtypes = []
+            for name, argtypes in SIGNATURES.items():
+                f = getattr(L, name)
+                f.argtypes = argtypes
+                f.restype = ctypes.c_int32
+            v = L.piton_mi355x_abi_version()
+            if v != ABI_VERSION:
+                raise RuntimeError(f"{path} has ABI {v}, expected {ABI_VERSION}")
+            _lib = L
+    return _lib
+
+
+def _call(name: str, *args) -> None:
+    L = lib()
+    rc = getattr(L, name)(*args)
+    if rc != OK:
+        msg = L.piton_mi355x_last_error().decode(errors="replace")
+        if rc == EINVAL:
+            raise ValueError(f"{name}: {msg}")
+        raise MI355XError(rc, f"{name}: {msg}")
+
+
+def device_info() -> dict:
+    info = DeviceInfo()
+    _call("piton_mi355x_device_info", ctypes.byref(info))
+    d = {k: getattr(info, k) for k, _ in DeviceInfo._fields_}
+    d["arch"] = info.arch.decode()
+    return d
+
+
+# -- argument checks ---------------------------------------------------------------------------
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _avail(t: torch.Tensor) -> int:
+    """Elements from t's first element to the end of its storage."""
+    return t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+
+
+def check_tensor(name: str, t, dtype=torch.float32, max_offset: int | None = None, allow_none=False):
+    """t must be a GPU tensor of `dtype` whose storage holds element offsets 0..max_offset."""
+    if t is None:
+        if allow_none:
+            return None
+        raise ValueError(f"{name}: a tensor is required")
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: tensor on {t.device}, expected a ROCm GPU tensor")
+    if max_offset is not None and max_offset >= 0 and max_offset >= _avail(t):
+        raise ValueError(f"{name}: the kernel addresses element {max_offset} but the storage holds "
+                         f"{_avail(t)} from the tensor's start")
+    return t
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _span(*pairs) -> int:
+    """Largest element offset sum((n_i - 1) * stride_i) of an access pattern; -1 if empty."""
+    off = 0
+    for n, s in pairs:
+        if n <= 0:
+            return -1
+        if s < 0:
+            raise ValueError("negative strides are not supported")
+        off += (n - 1) * s
+    return off
+
+
+# -- entries -------------------------------------------------------------------------------------
+
+def matmul(a, b, c, M, N, K, s_am, s_ak, s_bk, s_bn, s_cm, s_cn, group_size_m=8):
+    """C = A B (matmul_kernel, examples/kernels.py:18-57) on torch tensors."""
+    check_tensor("a", a, max_offset=_span((M, s_am), (K, s_ak)))
+    check_tensor("b", b, max_offset=_span((K, s_bk), (N, s_bn)))
+    check_tensor("c", c, max_offset=_span((M, s_cm), (N, s_cn)))
+    _call("piton_mi355x_matmul", _ptr(a), _ptr(b), _ptr(c), M, N, K, s_am, s_ak, s_bk, s_bn, s_cm, s_cn,
+          int(group_size_m), _stream())
+
+
+def softmax(out, inp, in_row_stride, out_row_stride, n_cols, n_rows, block_size):
+    """softmax_kernel (examples/kernels.py:60-76) over n_rows rows."""
+    n = min(int(n_cols), int(block_size))
+    check_tensor("input", inp, max_offset=_span((n_rows, in_row_stride), (n, 1)))
+    check_tensor("output", out, max_offset=_span((n_rows, out_row_stride), (n, 1)))
+    _call("piton_mi355x_softmax", _ptr(out), _ptr(inp), in_row_stride, out_row_stride, n_cols, n_rows,
+          int(block_size), _stream())
+
+
+def attn_fwd(q, k, v, out, sm_scale, s_qh, s_qm, s_kh, s_kn, s_kk, s_vh, s_vn, s_oh, s_om, n_ctx, heads,
+             head_dim, causal):
+    """attn_fwd_kernel (examples/attention.py:67-113) for `heads` heads."""
+    check_tensor("Q", q, max_offset=_span((heads, s_qh), (n_ctx, s_qm), (head_dim, 1)))
+    check_tensor("K", k, max_offset=_span((heads, s_kh), (n_ctx, s_kn), (head_dim, s_kk)))
+    check_tensor("V", v, max_offset=_span((heads, s_vh), (n_ctx, s_vn), (head_dim, 1)))
+    check_tensor("Out", out, max_offset=_span((heads, s_oh), (n_ctx, s_om), (head_dim, 1)))
+    _call("piton_mi355x_attn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(out), float(sm_scale), s_qh, s_qm, s_kh,
+          s_kn, s_kk, s_vh, s_vn, s_oh, s_om, n_ctx, heads, int(head_dim), int(bool(causal)), _stream())
+
+
+def dense(x, w, bias, y, M, N, K, add_bias=True, relu=False, argmax_out=None, n_classes=0):
+    """dense_layer_kernel (examples/nn_kernels.py:23-74): Y = [ReLU](X W [+ b]), with an
+    optional per-row argmax over the first n_classes outputs."""
+    check_tensor("x", x, max_offset=M * K - 1)
+    check_tensor("w", w, max_offset=K * N - 1)
+    check_tensor("bias", bias, max_offset=N - 1, allow_none=not add_bias)
+    check_tensor("y", y, max_offset=M * N - 1)
+    check_tensor("argmax", argmax_out, dtype=torch.int32, max_offset=M - 1, allow_none=True)
+    _call("piton_mi355x_dense", _ptr(x), _ptr(w), _ptr(bias if add_bias else None), _ptr(y), M, N, K,
+          int(bool(add_bias)), int(bool(relu)), _ptr(argmax_out), int(n_classes), _stream())
+
+
+def add(x, y, out, n):
+    """add_kernel (examples/kernels.py:6-15)."""
+    for name, t in (("x", x), ("y", y), ("output", out)):
+        check_tensor(name, t, max_offset=n - 1)
+    _call("piton_mi355x_add", _ptr(x), _ptr(y), _ptr(out), n, _stream())
+
+
+def layernorm(x, out, n, eps, rows, row_stride):
+    """layernorm_kernel (tests/test_reroll_reduce.py:199-208)."""
+    check_tensor("x", x, max_offset=_span((rows, row_stride), (n, 1)))
+    check_tensor("out", out, max_offset=_span((rows, row_stride), (n, 1)))
+    _call("piton_mi355x_layernorm", _ptr(x), _ptr(out), n, float(eps), rows, row_stride, _stream())
+
+
+def argmax_rows(x, rows, ld, n, out):
+    check_tensor("x", x, max_offset=_span((rows, ld), (n, 1)))
+    check_tensor("out", out, dtype=torch.int32, max_offset=rows - 1)
+    _call("piton_mi355x_argmax_rows", _ptr(x), rows, ld, n, _ptr(out), _stream())
+
+
+def embedding(ids, ids_ld, tok, pos, out, batch, T, d_model, vocab, pos_offset, err_flag=None):
+    check_tensor("ids", ids, dtype=torch.int32, max_offset=_span((batch, ids_ld), (T, 1)))
+    check_tensor("tok", tok, max_offset=vocab * d_model - 1)
+    check_tensor("pos", pos, max_offset=(pos_offset + T) * d_model - 1)
+    check_tensor("out", out, max_offset=batch * T * d_model - 1)
+    check_tensor("err_flag", err_flag, dtype=torch.int32, max_offset=0, allow_none=True)
+    _call("piton_mi355x_embedding", _ptr(ids), ids_ld, _ptr(tok), _ptr(pos), _ptr(out), batch, T, d_model, vocab,
+          pos_offset, _ptr(err_flag), _stream())

@@ -1,0 +1,146 @@
+"""Grouped matmul (examples/kernels.py:18-57) on the MI355X against the oracle.
+
+Bar: bit-exact on dyadic inputs (every product and partial sum exact, so any order gives the
+same bits; tests/test_nn_kernels.py:37-61 style); otherwise relative Frobenius error <= 1e-5
+vs float64 and no larger than the oracle's (the emulator's round-toward-zero chain)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import fp64
+from piton_amd import cdiv
+from piton_amd.kernels import matmul_kernel
+from piton_amd.runtime import mi355x as rt
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def run(a, b, c=None, group=8, block=(64, 64, 16)):
+    """matmul_kernel[grid] on torch tensors, with the reference's argument list."""
+    M, K = a.shape
+    N = b.shape[1]
+    if c is None:
+        c = torch.full((M, N), -1.0, device="cuda")
+    grid = (cdiv(M, block[0]) * cdiv(N, block[1]),)
+    matmul_kernel[grid](a, b, c, M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0),
+                        c.stride(1), BLOCK_SIZE_M=block[0], BLOCK_SIZE_N=block[1], BLOCK_SIZE_K=block[2],
+                        GROUP_SIZE_M=group, device="mi355x")
+    torch.cuda.synchronize()
+    return c
+
+
+def dyadic(rng, shape):
+    return (rng.integers(-4, 5, shape) / 4).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (72, 100, 64), (40, 70, 36), (16, 128, 32), (1, 1, 1),
+                                   (129, 257, 33), (300, 129, 515)])
+def test_dyadic_bit_exact(M, N, K):
+    rng = np.random.default_rng(M * 1000 + N + K)
+    a, b = dyadic(rng, (M, K)), dyadic(rng, (K, N))
+    c = run(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()).cpu().numpy()
+    np.testing.assert_array_equal(c, oracle.matmul(a, b))
+    np.testing.assert_array_equal(c, a @ b)
+
+
+@pytest.mark.parametrize("n", [512, 1024])
+def test_square_uniform(n):
+    rng = np.random.default_rng(n)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    c = run(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()).cpu().numpy()
+    ref = fp64.matmul(a, b)
+    emu = oracle.matmul_fast(a, b, threads=8)
+    err, err_emu = fp64.rel_fro(c, ref), fp64.rel_fro(emu, ref)
+    assert err <= TOL, err
+    assert err <= err_emu, (err, err_emu)
+
+
+def test_4096_sampled_rows():
+    """At the benchmark size the float64 check runs on 64 sampled rows of C (the kernel
+    computes them in tiles shared with every other row)."""
+    n = 4096
+    g = torch.Generator(device="cuda").manual_seed(7)
+    a = torch.rand((n, n), device="cuda", generator=g) * 2 - 1
+    b = torch.rand((n, n), device="cuda", generator=g) * 2 - 1
+    c = run(a, b)
+    rows = np.random.default_rng(1).choice(n, 64, replace=False)
+    an, bn = a.cpu().numpy(), b.cpu().numpy()
+    ref = fp64.matmul(an[rows], bn)
+    got = c.cpu().numpy()[rows]
+    emu = oracle.matmul_fast(an[rows], bn, threads=8)
+    assert fp64.rel_fro(got, ref) <= TOL
+    assert fp64.rel_fro(got, ref) <= fp64.rel_fro(emu, ref)
+
+
+@pytest.mark.parametrize("layout", ["padded", "b_transposed", "a_transposed", "odd_strides"])
+def test_ragged_runtime_strides(layout):
+    """The ragged 1000 x 1800 x 700 case with runtime strides; C's padding must stay
+    untouched (a guard band: the masked store)."""
+    M, N, K = 1000, 1800, 700
+    rng = np.random.default_rng(5)
+    a_np = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    b_np = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    if layout == "padded":
+        A = torch.zeros((M, K + 4), device="cuda"); A[:, :K] = torch.from_numpy(a_np)
+        B = torch.zeros((K, N + 4), device="cuda"); B[:, :N] = torch.from_numpy(b_np)
+        a, b = A[:, :K], B[:, :N]
+    elif layout == "b_transposed":
+        a = torch.from_numpy(a_np).cuda()
+        b = torch.from_numpy(np.ascontiguousarray(b_np.T)).cuda().t()  # stride_bk = 1
+    elif layout == "a_transposed":
+        a = torch.from_numpy(np.ascontiguousarray(a_np.T)).cuda().t()  # stride_am = 1
+        b = torch.from_numpy(b_np).cuda()
+    else:  # lda = 703, ldb = 1805: rows not 16-byte aligned -> scalar loaders
+        A = torch.zeros((M, K + 3), device="cuda"); A[:, :K] = torch.from_numpy(a_np)
+        B = torch.zeros((K, N + 5), device="cuda"); B[:, :N] = torch.from_numpy(b_np)
+        a, b = A[:, :K], B[:, :N]
+    C = torch.full((M + 2, N + 7), -7.0, device="cuda")
+    c = C[:M, :N]
+    run(a, b, c)
+    Cn = C.cpu().numpy()
+    ref = fp64.matmul(a_np, b_np)
+    assert fp64.rel_fro(Cn[:M, :N], ref) <= TOL
+    assert (Cn[M:, :] == -7.0).all() and (Cn[:, N:] == -7.0).all()
+
+
+def test_numpy_arrays_copy_in_copy_out():
+    """numpy arguments: copied to the device and every array copied back (launcher.py:209-211)."""
+    rng = np.random.default_rng(3)
+    a, b = dyadic(rng, (40, 36)), dyadic(rng, (36, 70))
+    c = np.full((40, 70), -1.0, np.float32)
+    a0, b0 = a.copy(), b.copy()
+    matmul_kernel[(cdiv(40, 8) * cdiv(70, 64),)](a, b, c, 40, 70, 36, 36, 1, 70, 1, 70, 1, BLOCK_SIZE_M=8,
+                                                 BLOCK_SIZE_N=64, BLOCK_SIZE_K=4, GROUP_SIZE_M=4,
+                                                 device="mi355x")
+    np.testing.assert_array_equal(c, a @ b)
+    np.testing.assert_array_equal(a, a0)
+    np.testing.assert_array_equal(b, b0)
+
+
+@pytest.mark.parametrize("group", [1, 3, 8, 64])
+def test_group_order_does_not_change_bits(group):
+    g = torch.Generator(device="cuda").manual_seed(11)
+    a = torch.rand((700, 500), device="cuda", generator=g)
+    b = torch.rand((500, 900), device="cuda", generator=g)
+    base = run(a, b, group=8)
+    other = run(a, b, group=group)
+    assert torch.equal(base, other)
+
+
+def test_empty_and_k_zero():
+    a = torch.zeros((5, 0), device="cuda")
+    b = torch.zeros((0, 7), device="cuda")
+    c = torch.full((5, 7), 3.0, device="cuda")
+    rt.matmul(a, b, c, 5, 7, 0, 0, 1, 7, 1, 7, 1)
+    torch.cuda.synchronize()
+    assert (c == 0).all()
+    rt.matmul(a, b, c, 0, 7, 0, 0, 1, 7, 1, 7, 1)  # nothing to do
+
+
+def test_out_of_storage_strides_are_rejected():
+    a = torch.zeros((8, 8), device="cuda")
+    with pytest.raises(ValueError):
+        rt.matmul(a, a, a, 8, 8, 9, 8, 1, 8, 1, 8, 1)

@@ -1,0 +1,117 @@
+"""Fused row softmax (examples/kernels.py:60-76) on the MI355X against the oracle.
+
+Bar: relative Frobenius error <= 1e-5 vs float64 over finite rows and no larger than the
+oracle's (the emulator's arithmetic); the NaN pattern of rows with special values matches
+numpy's; columns past min(n_cols, BLOCK_SIZE) are never written."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import fp64
+from piton_amd import next_power_of_2
+from piton_amd.kernels import softmax_kernel
+from piton_amd.runtime import mi355x as rt
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def run(x, n_cols=None, block=None, out=None):
+    rows, stride = x.shape
+    n_cols = stride if n_cols is None else n_cols
+    block = block or next_power_of_2(n_cols)
+    if out is None:
+        out = torch.full_like(x, float("nan"))
+    softmax_kernel[(rows,)](out, x, x.stride(0), out.stride(0), n_cols, BLOCK_SIZE=block, device="mi355x")
+    torch.cuda.synchronize()
+    return out
+
+
+def check(got, x, n_cols, block=None):
+    n = min(n_cols, block or n_cols)
+    ref = fp64.softmax(x, n_cols, block)
+    finite = np.isfinite(ref[:, :n]).all(axis=1)
+    np.testing.assert_array_equal(np.isnan(got[:, :n]), np.isnan(ref[:, :n]))
+    err = fp64.rel_fro(got[finite, :n], ref[finite, :n])
+    assert err <= TOL, err
+    return err
+
+
+@pytest.mark.parametrize("rows,cols,block", [(4, 64, 64), (3, 100, 128), (5, 16, 16), (7, 1, 1), (2, 3, 4)])
+def test_reference_shapes(rows, cols, block):
+    rng = np.random.default_rng(42 + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    got = run(torch.from_numpy(x).cuda(), cols, block).cpu().numpy()
+    check(got, x, cols, block)
+    emu = oracle.softmax(x, cols, block)
+    ref = fp64.softmax(x, cols, block)
+    assert fp64.rel_fro(got, ref) <= max(fp64.rel_fro(emu, ref), 1e-7)
+
+
+@pytest.mark.parametrize("n", [1024, 4096, 1823])
+def test_benchmark_shapes_with_special_rows(n):
+    """4096 rows x n of N(0,1)*4 with a +inf entry, a -inf entry, an all -inf row and a NaN
+    entry in a few rows; rows of 1823 are not 16-byte aligned."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((4096, n)) * 4).astype(np.float32)
+    x[3, 17] = np.inf
+    x[5, n - 1] = -np.inf
+    x[9, :] = -np.inf
+    x[11, 2] = np.nan
+    got = run(torch.from_numpy(x).cuda()).cpu().numpy()
+    check(got, x, n)
+    assert np.isnan(got[3]).all() and np.isnan(got[9]).all() and np.isnan(got[11]).all()
+    assert got[5, n - 1] == 0.0
+    finite_rows = np.isfinite(x).all(axis=1)
+    np.testing.assert_allclose(got[finite_rows].astype(np.float64).sum(axis=1), 1.0, rtol=0, atol=2e-6)
+    # the oracle's error on a sample of finite rows bounds the GPU's there
+    sample = np.flatnonzero(finite_rows)[:64]
+    emu = oracle.softmax(x[sample], n)
+    ref = fp64.softmax(x[sample])
+    assert fp64.rel_fro(got[sample], ref) <= fp64.rel_fro(emu, ref)
+
+
+def test_block_smaller_than_row_and_untouched_columns():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((6, 300)).astype(np.float32)
+    got = run(torch.from_numpy(x).cuda(), 300, 128).cpu().numpy()
+    check(got, x, 300, 128)
+    assert np.isnan(got[:, 128:]).all()
+
+
+@pytest.mark.parametrize("in_stride,out_stride,n", [(1823, 1823, 1823), (1825, 1830, 1823), (37, 41, 33),
+                                                    (4096, 4099, 4000)])
+def test_row_strides_and_alignments(in_stride, out_stride, n):
+    rows = 33
+    rng = np.random.default_rng(in_stride)
+    xin = torch.from_numpy(rng.standard_normal((rows, in_stride)).astype(np.float32)).cuda()
+    out = torch.full((rows, out_stride), -5.0, device="cuda")
+    rt.softmax(out, xin, in_stride, out_stride, n, rows, next_power_of_2(n))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    x = xin.cpu().numpy()
+    check(got[:, :n], x[:, :n], n)
+    assert (got[:, n:] == -5.0).all()
+
+
+def test_long_rows_take_the_multipass_kernel():
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal((5, 10000)) * 3).astype(np.float32)
+    got = run(torch.from_numpy(x).cuda()).cpu().numpy()
+    check(got, x, 10000)
+
+
+def test_in_place():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((64, 1000)).astype(np.float32)
+    t = torch.from_numpy(x).cuda()
+    run(t, out=t)
+    check(t.cpu().numpy(), x, 1000)
+
+
+def test_numpy_launch():
+    x = np.random.default_rng(4).standard_normal((3, 100)).astype(np.float32)
+    y = np.zeros_like(x)
+    softmax_kernel[(3,)](y, x, 100, 100, 100, BLOCK_SIZE=128, device="mi355x")
+    check(y, x, 100)

@@ -48,6 +48,35 @@ def timed(fn, iters, stream):
     return [s.elapsed_time(e) * 1e-3 for s, e in evs]
 
 
+def timed_graph(fn, iters, reps=3):
+    """Average duration (s) of fn(i), i = 0..iters-1, launched back to back from a captured HIP
+    graph (no host work between launches), timed with HIP events around each replay; the
+    median over `reps` replays."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(0)  # warm: library loaded, kernels resident
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(iters):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    out = []
+    stream = torch.cuda.current_stream()
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) * 1e-3 / iters)
+    return sorted(out)[len(out) // 2]
+
+
 def bench_matmul(n, steps, warmup):
     import torch
 
@@ -76,8 +105,9 @@ def bench_matmul(n, steps, warmup):
     return dict(wall=wall, durs=durs, flops=flops, a=a, b=b, c=c)
 
 
-def bench_softmax(n, rows=4096, reps=20):
-    """Cold-cache GB/s: buffer pairs rotated over > 512 MB so each launch reads from HBM."""
+def bench_softmax(n, rows=4096, launches=48):
+    """Cold-cache GB/s: buffer pairs rotated over > 512 MB so each launch reads from HBM; the
+    launches replay from a HIP graph, back to back."""
     import torch
 
     from piton_amd import next_power_of_2
@@ -92,31 +122,32 @@ def bench_softmax(n, rows=4096, reps=20):
     def step(i):
         rt.softmax(ys[i % pairs], xs[i % pairs], n, n, n, rows, block)
 
-    stream = torch.cuda.current_stream()
-    timed(step, pairs, stream)  # warm-up pass over every pair
-    durs = timed(step, max(reps, pairs), stream)
-    avg = sum(durs) / len(durs)
+    avg = timed_graph(step, max(launches, pairs))
     del xs, ys
     torch.cuda.empty_cache()
-    return dict(n=n, rows=rows, bytes=pair_bytes, us=avg * 1e6, gbs=pair_bytes / avg / 1e9,
-                frac=pair_bytes / avg / PEAK_HBM)
+    return dict(n=n, rows=rows, bytes=pair_bytes, us=round(avg * 1e6, 3), gbs=round(pair_bytes / avg / 1e9, 1),
+                frac=round(pair_bytes / avg / PEAK_HBM, 4))
 
 
-def bench_attention(reps=20):
+def bench_attention(launches=32):
     import torch
 
-    from piton_amd.kernels.attention import attention_flops, run_attention
+    from piton_amd.kernels.attention import attention_flops
+    from piton_amd.runtime import mi355x as rt
     H, N, D = 32, 1024, 64
     g = torch.Generator(device="cuda").manual_seed(4)
     q, k, v = (torch.randn((H, N, D), device="cuda", generator=g) for _ in range(3))
-    stream = torch.cuda.current_stream()
-    timed(lambda i: run_attention(q, k, v, causal=True, block_m=128, block_n=32), 3, stream)
-    durs = timed(lambda i: run_attention(q, k, v, causal=True, block_m=128, block_n=32), reps, stream)
-    avg = sum(durs) / len(durs)
+    out = torch.empty_like(q)
+    scale = 1.0 / D ** 0.5
+
+    def step(_i):
+        rt.attn_fwd(q, k, v, out, scale, N * D, D, N * D, D, 1, N * D, D, N * D, D, N, H, D, True)
+
+    avg = timed_graph(step, launches)
     flops = attention_flops(N, D, causal=True, heads=H)
     nbytes = 4 * 4 * H * N * D
-    return dict(shape=[H, N, D], causal=True, us=avg * 1e6, tflops=flops / avg / 1e12,
-                frac_mfma=flops / avg / PEAK_FP32_MFMA, gbs=nbytes / avg / 1e9)
+    return dict(shape=[H, N, D], causal=True, us=round(avg * 1e6, 3), tflops=round(flops / avg / 1e12, 3),
+                frac_mfma=round(flops / avg / PEAK_FP32_MFMA, 4), gbs=round(nbytes / avg / 1e9, 1))
 
 
 def cpu_baseline(a, b, budget_s=10.0):

@@ -1,9 +1,11 @@
 // Flash attention forward: attn_fwd_kernel + _attn_fwd_inner (examples/attention.py:33-113).
 //
 // Design (gfx950, fp32 MFMA v_mfma_f32_32x32x2_f32):
-//   * workgroup = 4 wavefronts = 128 query rows of one head; each wave owns 32 queries, the
-//     workgroup walks the keys in blocks of 32 staged through LDS (two buffers, prefetched
-//     into registers while the previous block is multiplied);
+//   * workgroup = 4 wavefronts = 64 query rows of one head: two query groups of 32, each split
+//     over two waves by key parity; the workgroup walks the keys in tiles of 64 (two 32-key
+//     MFMA blocks) staged through LDS (two buffers, the next tile prefetched into registers
+//     while the current one is multiplied); the two waves of a query group merge their
+//     partial softmax states through LDS at the end;
 //   * the score block is computed transposed, S^T = K Q^T (keys x queries), so a lane holds
 //     16 scores of ONE query (lane % 32): the row max and row sum are 15 in-lane operations
 //     plus one exchange with lane ^ 32, and the running max / sum / rescale factor of a query
@@ -24,8 +26,14 @@ namespace piton {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int ABN = 32;  // keys per block
-constexpr int ABM = 128; // queries per workgroup
+// widest head dimension that uses the register prefetch of the next tile
+#ifndef PITON_ATTN_PREFETCH_MAX_D
+#define PITON_ATTN_PREFETCH_MAX_D 64
+#endif
+
+constexpr int ABN = 32;  // keys per MFMA block
+constexpr int ABM = 64;  // queries per workgroup
+constexpr int AKT = 64;  // keys per LDS tile (two blocks: one per key parity)
 
 enum : int { K_VEC_D = 0, K_VEC_N = 1, K_SCALAR = 2 };
 
@@ -40,13 +48,20 @@ struct AttnArgs {
     int v_vec;  // V rows loadable as float4
 };
 
+// values per thread of one K (or V) tile of AKT keys x D
+template <int D>
+struct Tile {
+    static constexpr int kVals = AKT * D / 256;
+    static constexpr int kVec = kVals / 4;
+};
+
 template <int D, int KL>
 __device__ __forceinline__ void attn_load(const AttnArgs &g, int t, const float *kb, const float *vb, int64_t key0,
-                                          float (&rk)[D / 8], float (&rv)[D / 8]) {
-    // K tile: 32 keys x D -> 8 * D / 256 = D / 8 values per thread
+                                          float (&rk)[Tile<D>::kVals], float (&rv)[Tile<D>::kVals]) {
+    constexpr int NV = Tile<D>::kVec, NS = Tile<D>::kVals;
     if constexpr (KL == K_VEC_D) {
 #pragma unroll
-        for (int i = 0; i < D / 32; i++) {
+        for (int i = 0; i < NV; i++) {
             const int idx = t + 256 * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
             const int64_t n = key0 + key;
@@ -56,9 +71,9 @@ __device__ __forceinline__ void attn_load(const AttnArgs &g, int t, const float 
         }
     } else if constexpr (KL == K_VEC_N) {
 #pragma unroll
-        for (int i = 0; i < D / 32; i++) {
+        for (int i = 0; i < NV; i++) {
             const int idx = t + 256 * i;
-            const int d = idx / 8, kq = idx % 8;
+            const int d = idx / (AKT / 4), kq = idx % (AKT / 4);
             const int64_t n = key0 + 4 * kq;
             float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
             if (n < g.n_ctx && d < g.head_dim) f = *reinterpret_cast<const float4 *>(kb + d * g.s_kk + n);
@@ -66,17 +81,16 @@ __device__ __forceinline__ void attn_load(const AttnArgs &g, int t, const float 
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < D / 8; i++) {
+        for (int i = 0; i < NS; i++) {
             const int idx = t + 256 * i;
             const int key = idx / D, d = idx % D;
             const int64_t n = key0 + key;
             rk[i] = (n < g.n_ctx && d < g.head_dim) ? kb[n * g.s_kn + d * g.s_kk] : 0.f;
         }
     }
-    // V tile: rows contiguous along d
     if (g.v_vec) {
 #pragma unroll
-        for (int i = 0; i < D / 32; i++) {
+        for (int i = 0; i < NV; i++) {
             const int idx = t + 256 * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
             const int64_t n = key0 + key;
@@ -86,7 +100,7 @@ __device__ __forceinline__ void attn_load(const AttnArgs &g, int t, const float 
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < D / 8; i++) {
+        for (int i = 0; i < NS; i++) {
             const int idx = t + 256 * i;
             const int key = idx / D, d = idx % D;
             const int64_t n = key0 + key;
@@ -96,11 +110,12 @@ __device__ __forceinline__ void attn_load(const AttnArgs &g, int t, const float 
 }
 
 template <int D, int KL>
-__device__ __forceinline__ void attn_store(const AttnArgs &g, int t, float (&Ks)[ABN][D + 1], float (&Vs)[ABN][D],
-                                           const float (&rk)[D / 8], const float (&rv)[D / 8]) {
+__device__ __forceinline__ void attn_store(const AttnArgs &g, int t, float (*Ks)[D + 1], float (*Vs)[D],
+                                           const float (&rk)[Tile<D>::kVals], const float (&rv)[Tile<D>::kVals]) {
+    constexpr int NV = Tile<D>::kVec, NS = Tile<D>::kVals;
     if constexpr (KL == K_VEC_D) {
 #pragma unroll
-        for (int i = 0; i < D / 32; i++) {
+        for (int i = 0; i < NV; i++) {
             const int idx = t + 256 * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
 #pragma unroll
@@ -108,45 +123,57 @@ __device__ __forceinline__ void attn_store(const AttnArgs &g, int t, float (&Ks)
         }
     } else if constexpr (KL == K_VEC_N) {
 #pragma unroll
-        for (int i = 0; i < D / 32; i++) {
+        for (int i = 0; i < NV; i++) {
             const int idx = t + 256 * i;
-            const int d = idx / 8, kq = idx % 8;
+            const int d = idx / (AKT / 4), kq = idx % (AKT / 4);
 #pragma unroll
             for (int j = 0; j < 4; j++) Ks[4 * kq + j][d] = rk[4 * i + j];
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < D / 8; i++) {
+        for (int i = 0; i < NS; i++) {
             const int idx = t + 256 * i;
             Ks[idx / D][idx % D] = rk[i];
         }
     }
     if (g.v_vec) {
 #pragma unroll
-        for (int i = 0; i < D / 32; i++) {
+        for (int i = 0; i < NV; i++) {
             const int idx = t + 256 * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
             *reinterpret_cast<float4 *>(&Vs[key][4 * dq]) = make_float4(rv[4 * i], rv[4 * i + 1], rv[4 * i + 2], rv[4 * i + 3]);
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < D / 8; i++) {
+        for (int i = 0; i < NS; i++) {
             const int idx = t + 256 * i;
             Vs[idx / D][idx % D] = rv[i];
         }
     }
 }
 
+// Workgroup: 64 queries of one head; wave w = (query group w / 2, key parity w % 2). Each
+// iteration stages 64 keys (two 32-key blocks) in LDS; wave (g, p) multiplies block p of the
+// tile for its 32 queries, so the two waves of a query group split the keys and each walks
+// half as many blocks. Their running (max, sum, O) merge through LDS at the end.
 template <int D, int KL>
-__global__ __launch_bounds__(256) void attn_fwd_kernel_f32(AttnArgs g) {
-    __shared__ float Ks[2][ABN][D + 1];
-    __shared__ float Vs[2][ABN][D];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1)))
+void attn_fwd_kernel_f32(AttnArgs g) {
+    // D <= 64: two LDS buffers and the next tile prefetched into registers during the
+    // current tile's products; D = 128: one buffer, loaded between two barriers (the
+    // registers the prefetch would hold are the accumulators' at this width)
+    constexpr bool kPrefetch = D <= PITON_ATTN_PREFETCH_MAX_D;
+    constexpr int KS = AKT * (D + 1), VS = AKT * D, NBUF = kPrefetch ? 2 : 1;
+    __shared__ float smem[NBUF * (KS + VS)];
+    auto kt = [&](int buf) { return reinterpret_cast<float(*)[D + 1]>(smem + buf * (KS + VS)); };
+    auto vt = [&](int buf) { return reinterpret_cast<float(*)[D]>(smem + buf * (KS + VS) + KS); };
 
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, half = lane >> 5, l31 = lane & 31;
+    const int grp = wave >> 1, par = wave & 1;
     const int qb = g.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;  // longest first
     const int64_t h = blockIdx.y;
-    const int64_t q0 = (int64_t)qb * ABM + wave * 32;  // this wave's first query
-    const int64_t qi = q0 + l31;                        // this lane's query
+    const int64_t q0 = (int64_t)qb * ABM + grp * 32;  // this wave's first query
+    const int64_t qi = q0 + l31;                       // this lane's query
 
     const float *qp = g.q + h * g.s_qh;
     const float *kbase = g.k + h * g.s_kh;
@@ -169,34 +196,46 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel_f32(AttnArgs g) {
 
     const int64_t nkb_all = (g.n_ctx + ABN - 1) / ABN;
     const int64_t nkb = g.causal ? min(nkb_all, (int64_t)(qb + 1) * (ABM / ABN)) : nkb_all;
+    const int64_t nit = (nkb + 1) / 2;
     const int64_t wave_last = g.causal ? (q0 + 31) / ABN : nkb_all - 1;  // last block this wave needs
 
-    float rk[D / 8], rv[D / 8];
-    attn_load<D, KL>(g, t, kbase, vbase, 0, rk, rv);
-    attn_store<D, KL>(g, t, Ks[0], Vs[0], rk, rv);
-    __syncthreads();
+    float rk[Tile<D>::kVals], rv[Tile<D>::kVals];
+    if (kPrefetch) {
+        attn_load<D, KL>(g, t, kbase, vbase, 0, rk, rv);
+        attn_store<D, KL>(g, t, kt(0), vt(0), rk, rv);
+        __syncthreads();
+    }
 
-    for (int64_t kb = 0; kb < nkb; kb++) {
-        const int cur = (int)(kb & 1);
-        const bool more = kb + 1 < nkb;
-        if (more) attn_load<D, KL>(g, t, kbase, vbase, (kb + 1) * ABN, rk, rv);
+    for (int64_t it = 0; it < nit; it++) {
+        const int cur = kPrefetch ? (int)(it & 1) : 0;
+        const bool more = kPrefetch && it + 1 < nit;
+        if (more) attn_load<D, KL>(g, t, kbase, vbase, (it + 1) * AKT, rk, rv);
+        if (!kPrefetch) {
+            attn_load<D, KL>(g, t, kbase, vbase, it * AKT, rk, rv);
+            attn_store<D, KL>(g, t, kt(0), vt(0), rk, rv);
+            __syncthreads();
+        }
 
-        if (kb <= wave_last) {
+        const int64_t kb = 2 * it + par;
+        if (kb < nkb && kb <= wave_last) {
+            float(*Kt)[D + 1] = kt(cur) + par * ABN;
+            float(*Vt)[D] = vt(cur) + par * ABN;
             // S^T block: A = K [key][d], B = Q'^T
             f32x16 st;
 #pragma unroll
             for (int r = 0; r < 16; r++) st[r] = 0.f;
 #pragma unroll
             for (int s = 0; s < D / 2; s++)
-                st = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[cur][l31][2 * s + half], qf[s], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_32x32x2f32(Kt[l31][2 * s + half], qf[s], st, 0, 0, 0);
 
             // masks: register r holds key kb*32 + 8*(r/4) + 4*half + r%4 of query qi
-            const int64_t key0 = kb * ABN + 4 * half;
+            // key indices fit 32 bits (N_CTX < 2^31 is checked on the host)
+            const int key0 = (int)kb * ABN + 4 * half, n_ctx = (int)g.n_ctx, qi32 = (int)qi;
             float mloc = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t key = key0 + 8 * (r >> 2) + (r & 3);
-                if (key >= g.n_ctx || (g.causal && key > qi)) st[r] = -INFINITY;
+                const int key = key0 + 8 * (r >> 2) + (r & 3);
+                if (key >= n_ctx || (g.causal && key > qi32)) st[r] = -INFINITY;
                 mloc = fmaxf(mloc, st[r]);
             }
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
@@ -222,24 +261,42 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel_f32(AttnArgs g) {
 #pragma unroll
                 for (int s = 0; s < 16; s++) {
                     const int key = (s >> 2) * 8 + 4 * half + (s & 3);
-                    o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[cur][key][b * 32 + l31], st[s], o[b], 0, 0, 0);
+                    o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vt[key][b * 32 + l31], st[s], o[b], 0, 0, 0);
                 }
             }
         }
 
-        if (more) attn_store<D, KL>(g, t, Ks[cur ^ 1], Vs[cur ^ 1], rk, rv);
+        if (more) attn_store<D, KL>(g, t, kt(cur ^ 1), vt(cur ^ 1), rk, rv);
         __syncthreads();
     }
 
-    if (qi < g.n_ctx) {
-        const float inv = 1.0f / l_i;
+    // merge the key-parity halves of each query group: parity-1 waves hand (m, l, O) over LDS
+    // (same lane = same query and output element), parity-0 waves combine and store
+    float *xo = smem;                              // [grp][D/2 values][64 lanes]
+    float *xm = smem + 2 * (D / 2) * 64;           // [grp][2][64]
+    if (par == 1) {
+#pragma unroll
+        for (int b = 0; b < D / 32; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) xo[(grp * (D / 2) + b * 16 + r) * 64 + lane] = o[b][r];
+        xm[(grp * 2 + 0) * 64 + lane] = m_i;
+        xm[(grp * 2 + 1) * 64 + lane] = l_i;
+    }
+    __syncthreads();
+    if (par == 0 && qi < g.n_ctx) {
+        const float m_b = xm[(grp * 2 + 0) * 64 + lane], l_b = xm[(grp * 2 + 1) * 64 + lane];
+        const float m = fmaxf(m_i, m_b);
+        const float mu = m == -INFINITY ? 0.f : m;
+        const float ca = __builtin_amdgcn_exp2f(m_i - mu), cb = __builtin_amdgcn_exp2f(m_b - mu);
+        const float inv = 1.0f / (l_i * ca + l_b * cb);
         float *op = g.o + h * g.s_oh + qi * g.s_om;
 #pragma unroll
         for (int b = 0; b < D / 32; b++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int d = b * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (d < g.head_dim) op[d] = o[b][r] * inv;
+                const float ob = xo[(grp * (D / 2) + b * 16 + r) * 64 + lane];
+                if (d < g.head_dim) op[d] = (o[b][r] * ca + ob * cb) * inv;
             }
     }
 }
@@ -266,6 +323,7 @@ extern "C" int32_t piton_mi355x_attn_fwd(const float *q, const float *k, const f
     PITON_REQUIRE(aligned4(q) && aligned4(k) && aligned4(v) && aligned4(out), PITON_EINVAL,
                   "attn_fwd: pointers must be 4-byte aligned");
     PITON_REQUIRE(n_heads <= 65535, PITON_EUNSUPPORTED, "attn_fwd: %lld heads exceed grid axis 1", (long long)n_heads);
+    PITON_REQUIRE(n_ctx < (1LL << 31) - 64, PITON_EUNSUPPORTED, "attn_fwd: N_CTX %lld too large", (long long)n_ctx);
     int rc = require_device();
     if (rc) return rc;
     if (n_ctx == 0 || n_heads == 0) return PITON_OK;

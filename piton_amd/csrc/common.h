@@ -6,7 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/piton_mi355x.h"
+#include "piton_mi355x.h"
 
 namespace piton {
 

@@ -1,10 +1,12 @@
 // Row softmax: softmax_kernel (examples/kernels.py:60-76), HBM-bound.
 //
 // Design (gfx950):
-//   * one 64-lane wavefront per row, four rows per 256-thread workgroup, no LDS and no
-//     barriers: the row is loaded once into registers (CH float4 chunks per lane), reduced
-//     twice with DPP lane moves (max, then sum), and written once: 8 bytes of HBM traffic per
-//     element, the minimum;
+//   * one 64-lane wavefront per row at a time, four wavefronts per 256-thread workgroup, no
+//     LDS and no barriers: the row is loaded once into registers (CH float4 chunks per lane),
+//     reduced twice with DPP lane moves (max, then sum), and written once: 8 bytes of HBM
+//     traffic per element, the minimum. Rows of 8+ chunks per lane go two to a wavefront,
+//     the second row's loads issued before the first row is reduced and written;
+//   * loads and stores are nontemporal: the row is touched once;
 //   * rows need not be 16-byte aligned (n = 1823): each row is read through the aligned
 //     float4 window that covers it, and elements outside [0, n) of the row are masked to
 //     -inf. An aligned 16-byte block lies inside one page, so the window never touches an
@@ -14,7 +16,7 @@
 //     so each e^x is within about 1 ulp; the row sum's reciprocal is correctly rounded;
 //   * special values follow IEEE/numpy: a +inf or NaN entry, or an all -inf row, makes the
 //     whole row NaN; a -inf entry in a finite row gives exactly 0;
-//   * rows longer than 8189 columns take a workgroup-per-row kernel that reads the row three
+//   * rows longer than 4093 columns take a workgroup-per-row kernel that reads the row three
 //     times (max, sum, write).
 #include "common.h"
 
@@ -30,74 +32,104 @@ __device__ __forceinline__ float exp_acc(float d) {
     return fmaf(e, lo * 0.69314718055994531f, e);
 }
 
-template <int CH>
-__global__ __launch_bounds__(256) void softmax_rows_kernel(float *out, const float *in, int64_t in_rs, int64_t out_rs,
-                                                           int64_t n, int64_t rows) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-    if (row >= rows) return;  // whole wavefront leaves together
-    const float *rp = in + row * in_rs;
-    const int off = (int)((reinterpret_cast<uintptr_t>(rp) >> 2) & 3);
+// Loads row r's aligned float4 window (CH chunks per lane) into b; elements of the window
+// outside the row are masked when the row is processed.
+template <int CH, bool ALIGNED>
+__device__ __forceinline__ void load_row(const float *in, int64_t in_rs, int64_t r, int n, int lane,
+                                         f32x4 (&b)[CH], int &off) {
+    const float *rp = in + r * in_rs;
+    off = ALIGNED ? 0 : (int)((reinterpret_cast<uintptr_t>(rp) >> 2) & 3);
     const f32x4 *src = reinterpret_cast<const f32x4 *>(rp - off);
-    const int64_t nch = (off + n + 3) >> 2;
-
-    float v[CH][4];
-    float mx = -INFINITY;
+    const int nch = (off + n + 3) >> 2;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
-        const int64_t ci = lane + 64 * c;
+        const int ci = lane + 64 * c;
         f32x4 f = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         if (ci < nch) f = __builtin_nontemporal_load(src + ci);
-        const int64_t e0 = 4 * ci - off;
-        v[c][0] = (e0 >= 0 && e0 < n) ? f.x : -INFINITY;
-        v[c][1] = (e0 + 1 >= 0 && e0 + 1 < n) ? f.y : -INFINITY;
-        v[c][2] = (e0 + 2 >= 0 && e0 + 2 < n) ? f.z : -INFINITY;
-        v[c][3] = (e0 + 3 < n) ? f.w : -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 4; j++) mx = fmaxf(mx, v[c][j]);
+        b[c] = f;
     }
-    const float m = wave_reduce(mx, MaxOp());
+}
 
-    float s = 0.f;
-#pragma unroll
-    for (int c = 0; c < CH; c++) {
-        const int64_t e0 = 4 * (int64_t)(lane + 64 * c) - off;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const bool ok = e0 + j >= 0 && e0 + j < n;
-            const float e = ok ? exp_acc(v[c][j] - m) : 0.f;
-            v[c][j] = e;
-            s += e;
-        }
-    }
-    s = wave_reduce(s, SumOp());
-    const float inv = 1.0f / s;
+// RPW consecutive rows per wavefront: the next row's loads are issued before the current row
+// is reduced and stored, so every wave keeps reads in flight while it writes.
+// ALIGNED: every row of in and out starts 16-byte aligned and n % 4 == 0, so windows are the
+// rows themselves and only whole chunks need a bound. Rows here are < 8190 columns: element
+// indices inside a row fit 32 bits.
+template <int CH, int RPW, bool ALIGNED>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(float *out, const float *in, int64_t in_rs, int64_t out_rs,
+                                                           int n, int64_t rows) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RPW;
+    if (r0 >= rows) return;  // whole wavefront leaves together
+    const int64_t r1 = r0 + RPW < rows ? r0 + RPW : rows;
 
-    float *op = out + row * out_rs;
-    const int ooff = (int)((reinterpret_cast<uintptr_t>(op) >> 2) & 3);
-    if (ooff == off) {
-        f32x4 *dst = reinterpret_cast<f32x4 *>(op - off);
+    f32x4 cur[CH], nxt[CH];
+    int off, off_next = 0;
+    load_row<CH, ALIGNED>(in, in_rs, r0, n, lane, cur, off);
+    for (int64_t row = r0; row < r1; row++) {
+        if (RPW > 1 && row + 1 < r1) load_row<CH, ALIGNED>(in, in_rs, row + 1, n, lane, nxt, off_next);
+        const int nch = (off + n + 3) >> 2;
+        // mask the window to the row in place (-inf outside [0, n))
+        float mx = -INFINITY;
 #pragma unroll
         for (int c = 0; c < CH; c++) {
-            const int64_t ci = lane + 64 * c;
-            if (ci >= nch) continue;
-            const int64_t e0 = 4 * ci - off;
-            if (e0 >= 0 && e0 + 3 < n) {
-                const f32x4 w = {v[c][0] * inv, v[c][1] * inv, v[c][2] * inv, v[c][3] * inv};
-                __builtin_nontemporal_store(w, dst + ci);
+            const int e0 = 4 * (lane + 64 * c) - off;
+            if (ALIGNED) {
+                if (e0 >= n) cur[c] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    if (e0 + j >= 0 && e0 + j < n) op[e0 + j] = v[c][j] * inv;
+                    if (!(e0 + j >= 0 && e0 + j < n)) cur[c][j] = -INFINITY;
             }
+            mx = fmaxf(mx, fmaxf(fmaxf(cur[c].x, cur[c].y), fmaxf(cur[c].z, cur[c].w)));
         }
-    } else {
+        const float m = wave_reduce(mx, MaxOp());
+
+        float s = 0.f;
 #pragma unroll
         for (int c = 0; c < CH; c++) {
-            const int64_t e0 = 4 * (int64_t)(lane + 64 * c) - off;
+            const int e0 = 4 * (lane + 64 * c) - off;
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (e0 + j >= 0 && e0 + j < n) op[e0 + j] = v[c][j] * inv;
+            for (int j = 0; j < 4; j++) {
+                const bool ok = ALIGNED ? e0 < n : (e0 + j >= 0 && e0 + j < n);
+                const float e = ok ? exp_acc(cur[c][j] - m) : 0.f;
+                cur[c][j] = e;
+                s += e;
+            }
+        }
+        s = wave_reduce(s, SumOp());
+        const float inv = 1.0f / s;
+
+        float *op = out + row * out_rs;
+        const int ooff = ALIGNED ? 0 : (int)((reinterpret_cast<uintptr_t>(op) >> 2) & 3);
+        if (ooff == off) {
+            f32x4 *dst = reinterpret_cast<f32x4 *>(op - off);
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                const int ci = lane + 64 * c;
+                if (ci >= nch) continue;
+                const int e0 = 4 * ci - off;
+                if (ALIGNED || (e0 >= 0 && e0 + 3 < n)) {
+                    __builtin_nontemporal_store(cur[c] * inv, dst + ci);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (e0 + j >= 0 && e0 + j < n) op[e0 + j] = cur[c][j] * inv;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                const int e0 = 4 * (lane + 64 * c) - off;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (e0 + j >= 0 && e0 + j < n) op[e0 + j] = cur[c][j] * inv;
+            }
+        }
+        if (RPW > 1) {
+#pragma unroll
+            for (int c = 0; c < CH; c++) cur[c] = nxt[c];
+            off = off_next;
         }
     }
 }
@@ -152,19 +184,33 @@ extern "C" int32_t piton_mi355x_softmax(float *out, const float *in, int64_t in_
     const bool all_aligned = aligned16(in) && (in_row_stride % 4 == 0 || n_rows == 1);
     const int64_t nch = (n + 3 + (all_aligned ? 0 : 3)) / 4;
     const int64_t per_lane = (nch + 63) / 64;
-    const dim3 grid((unsigned)((n_rows + 3) / 4)), block(256);
+    const dim3 block(256);
+    // two rows per wave once a row is 8+ chunks per lane (measured: the next row's reads
+    // overlap the current row's writes); one row per wave for short rows
+    const dim3 grid1((unsigned)((n_rows + 3) / 4)), grid2((unsigned)((n_rows + 7) / 8));
     PITON_REQUIRE(n_rows <= 0x7FFFFFFFLL * 4, PITON_EUNSUPPORTED, "softmax: too many rows");
-    if (per_lane <= 1) hipLaunchKernelGGL(softmax_rows_kernel<1>, grid, block, 0, st, out, in, in_row_stride, out_row_stride, n, n_rows);
-    else if (per_lane <= 2) hipLaunchKernelGGL(softmax_rows_kernel<2>, grid, block, 0, st, out, in, in_row_stride, out_row_stride, n, n_rows);
-    else if (per_lane <= 4) hipLaunchKernelGGL(softmax_rows_kernel<4>, grid, block, 0, st, out, in, in_row_stride, out_row_stride, n, n_rows);
-    else if (per_lane <= 8) hipLaunchKernelGGL(softmax_rows_kernel<8>, grid, block, 0, st, out, in, in_row_stride, out_row_stride, n, n_rows);
-    else if (per_lane <= 16) hipLaunchKernelGGL(softmax_rows_kernel<16>, grid, block, 0, st, out, in, in_row_stride, out_row_stride, n, n_rows);
-    else if (per_lane <= 32) hipLaunchKernelGGL(softmax_rows_kernel<32>, grid, block, 0, st, out, in, in_row_stride, out_row_stride, n, n_rows);
+    const bool aligned = aligned16(in) && aligned16(out) && n % 4 == 0 &&
+                         ((in_row_stride % 4 == 0 && out_row_stride % 4 == 0) || n_rows == 1);
+#define PITON_SM(CH, RPW, G)                                                                                        \
+    do {                                                                                                            \
+        if (aligned)                                                                                                \
+            hipLaunchKernelGGL((softmax_rows_kernel<CH, RPW, true>), G, block, 0, st, out, in, in_row_stride,       \
+                               out_row_stride, (int)n, n_rows);                                                     \
+        else                                                                                                        \
+            hipLaunchKernelGGL((softmax_rows_kernel<CH, RPW, false>), G, block, 0, st, out, in, in_row_stride,      \
+                               out_row_stride, (int)n, n_rows);                                                     \
+    } while (0)
+    if (per_lane <= 1) PITON_SM(1, 1, grid1);
+    else if (per_lane <= 2) PITON_SM(2, 1, grid1);
+    else if (per_lane <= 4) PITON_SM(4, 1, grid1);
+    else if (per_lane <= 8) PITON_SM(8, 2, grid2);
+    else if (per_lane <= 16) PITON_SM(16, 2, grid2);
     else {
         PITON_REQUIRE(n_rows <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "softmax: too many rows");
         hipLaunchKernelGGL(softmax_long_kernel, dim3((unsigned)n_rows), block, 0, st, out, in, in_row_stride,
                            out_row_stride, n);
     }
+#undef PITON_SM
     rc = check_launch("softmax");
     if (rc == PITON_OK) clear_error();
     return rc;

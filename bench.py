@@ -150,6 +150,38 @@ def bench_attention(launches=32):
                 frac_mfma=round(flops / avg / PEAK_FP32_MFMA, 4), gbs=round(nbytes / avg / 1e9, 1))
 
 
+def bench_mlp(reps=3):
+    """Digits MLP 64 -> 128 -> 64 -> 10 over a batch of 1797: three dense launches and the
+    fused argmax, replayed from a HIP graph."""
+    import numpy as np
+    import torch
+
+    from piton_amd import digits
+    layers = digits.he_normal_mlp(seed=1729)
+    mlp = digits.MLP(layers, max_batch=1797)
+    x = torch.from_numpy(np.random.default_rng(0).integers(0, 17, (1797, 64)).astype(np.float32)).cuda()
+    avg = timed_graph(lambda i: mlp.run(x), 16, reps)
+    return dict(batch=1797, us=round(avg * 1e6, 3), images_per_s=round(1797 / avg, 1))
+
+
+def bench_tinygpt():
+    """TinyGPT greedy decoding: 64 prompts x 32 tokens, 128 new tokens each, K/V cache; the
+    whole generate() call (host loop and launches included)."""
+    import torch
+
+    from piton_amd import tinygpt
+    w = tinygpt.init_weights(seed=0)
+    prompts = tinygpt.seeded_prompts()
+    model = tinygpt.TinyGPT(w, batch=64)
+    model.generate(prompts, 128)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    model.generate(prompts, 128)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return dict(sequences=64, prompt=32, new_tokens=128, s=round(dt, 4), tokens_per_s=round(64 * 128 / dt, 1))
+
+
 def cpu_baseline(a, b, budget_s=10.0):
     """The oracle's matmul (round-toward-zero restatement, vectorised, all host threads up to
     16) on the first rows of the same product; rows grow until about budget_s of work."""
@@ -218,6 +250,8 @@ def main():
     if not args.no_extras:
         line["softmax"] = [bench_softmax(nc) for nc in (1024, 4096, 1823)]
         line["attention"] = bench_attention()
+        line["mlp"] = bench_mlp()
+        line["tinygpt"] = bench_tinygpt()
     print(json.dumps(line))
 
 

@@ -112,13 +112,45 @@ PITON_API int32_t piton_mi355x_argmax_rows(const float *x, int64_t rows, int64_t
                                  int32_t *out, void *stream);
 
 /* Token + position embedding gather. No reference counterpart (the reference has no decoder
- * model): out[b, t, :] = tok[ids[b, t], :] + pos[pos_offset + t, :], ids [batch, T] with
- * row stride ids_ld; rows of out are d_model apart. Ids outside [0, vocab) are an error
- * reported through err_flag (set to 1; the row is written as NaN). */
-PITON_API int32_t piton_mi355x_embedding(const int32_t *ids, int64_t ids_ld, const float *tok,
-                               const float *pos, float *out, int64_t batch, int64_t T,
-                               int64_t d_model, int64_t vocab, int64_t pos_offset,
+ * model): out[b, t, :] = tok[ids[b, t], :] + pos[pos_offset + t, :] for b < batch, t < T, with
+ * ids[b, t] at ids[b*ids_sb + t*ids_st] and out[b, t, c] at out[b*out_sb + t*out_st + c]; tok is
+ * [vocab, d_model] and pos [>= pos_offset + T, d_model], contiguous. An id outside [0, vocab)
+ * writes NaN and sets *err_flag = 1 (err_flag may be NULL). */
+PITON_API int32_t piton_mi355x_embedding(const int32_t *ids, int64_t ids_sb, int64_t ids_st, const float *tok,
+                               const float *pos, float *out, int64_t out_sb, int64_t out_st, int64_t batch,
+                               int64_t T, int64_t d_model, int64_t vocab, int64_t pos_offset,
                                int32_t *err_flag, void *stream);
+
+/* Y[M,N] = [ReLU](X[M,K] W[K,N] [+ bias]) [+ residual], X, Y and residual rows at strides ldx,
+ * ldy, ldr (W contiguous). The decoder's projections: the residual add of a transformer block is
+ * fused into the epilogue (residual may equal Y). Generalises dense_layer_kernel
+ * (examples/nn_kernels.py:23-74) to strided rows and the residual; bias and residual may be
+ * NULL. */
+PITON_API int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *w, const float *bias,
+                            const float *residual, int64_t ldr, float *y, int64_t ldy, int64_t M,
+                            int64_t N, int64_t K, int32_t relu, void *stream);
+
+/* attn_fwd_kernel (examples/attention.py:67-113) over batch x n_heads heads: grid row y is
+ * head y % n_heads of batch y / n_heads, whose Q / K / V / Out start at b*stride_?b + h*stride_?h.
+ * piton_mi355x_attn_fwd is the batch = 1 case. */
+PITON_API int32_t piton_mi355x_attn_fwd_batched(const float *q, const float *k, const float *v, float *out,
+                                      float sm_scale, int64_t stride_qb, int64_t stride_qh,
+                                      int64_t stride_qm, int64_t stride_kb, int64_t stride_kh,
+                                      int64_t stride_kn, int64_t stride_kk, int64_t stride_vb,
+                                      int64_t stride_vh, int64_t stride_vn, int64_t stride_ob,
+                                      int64_t stride_oh, int64_t stride_om, int64_t n_ctx, int64_t batch,
+                                      int64_t n_heads, int32_t head_dim, int32_t causal, void *stream);
+
+/* One new query per (batch, head) attending to keys 0 .. n_keys-1 of a K/V cache: the decode
+ * step of a KV-cached decoder, equal to the last query row of attn_fwd with causal masking over
+ * n_keys keys. Rows of q, k, v, out are contiguous along head_dim; n_keys <= 8192. No reference
+ * counterpart (the reference has no decoder). */
+PITON_API int32_t piton_mi355x_attn_decode(const float *q, const float *k, const float *v, float *out,
+                                 float sm_scale, int64_t stride_qb, int64_t stride_qh, int64_t stride_kb,
+                                 int64_t stride_kh, int64_t stride_kn, int64_t stride_vb,
+                                 int64_t stride_vh, int64_t stride_vn, int64_t stride_ob,
+                                 int64_t stride_oh, int64_t n_keys, int64_t batch, int64_t n_heads,
+                                 int32_t head_dim, void *stream);
 
 #ifdef __cplusplus
 }

@@ -43,6 +43,8 @@ struct AttnArgs {
     float scale;  // sm_scale * log2(e)
     int64_t s_qh, s_qm, s_kh, s_kn, s_kk, s_vh, s_vn, s_oh, s_om;
     int64_t n_ctx;
+    int64_t s_qb, s_kb, s_vb, s_ob;  // batch strides: grid row y is (batch y / n_heads, head y % n_heads)
+    int64_t n_heads;
     int head_dim;
     int causal;
     int v_vec;  // V rows loadable as float4
@@ -171,13 +173,13 @@ void attn_fwd_kernel_f32(AttnArgs g) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, half = lane >> 5, l31 = lane & 31;
     const int grp = wave >> 1, par = wave & 1;
     const int qb = g.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;  // longest first
-    const int64_t h = blockIdx.y;
+    const int64_t bh = blockIdx.y, bi = bh / g.n_heads, h = bh % g.n_heads;
     const int64_t q0 = (int64_t)qb * ABM + grp * 32;  // this wave's first query
     const int64_t qi = q0 + l31;                       // this lane's query
 
-    const float *qp = g.q + h * g.s_qh;
-    const float *kbase = g.k + h * g.s_kh;
-    const float *vbase = g.v + h * g.s_vh;
+    const float *qp = g.q + bi * g.s_qb + h * g.s_qh;
+    const float *kbase = g.k + bi * g.s_kb + h * g.s_kh;
+    const float *vbase = g.v + bi * g.s_vb + h * g.s_vh;
 
     // Q'^T fragments: B[k = d][n = query] for d = 2s + half, scaled by sm_scale * log2 e
     float qf[D / 2];
@@ -289,7 +291,7 @@ void attn_fwd_kernel_f32(AttnArgs g) {
         const float mu = m == -INFINITY ? 0.f : m;
         const float ca = __builtin_amdgcn_exp2f(m_i - mu), cb = __builtin_amdgcn_exp2f(m_b - mu);
         const float inv = 1.0f / (l_i * ca + l_b * cb);
-        float *op = g.o + h * g.s_oh + qi * g.s_om;
+        float *op = g.o + bi * g.s_ob + h * g.s_oh + qi * g.s_om;
 #pragma unroll
         for (int b = 0; b < D / 32; b++)
 #pragma unroll
@@ -308,38 +310,160 @@ static void launch_d(int kl, const AttnArgs &g, dim3 grid, hipStream_t st) {
     else hipLaunchKernelGGL((attn_fwd_kernel_f32<D, K_SCALAR>), grid, dim3(256), 0, st, g);
 }
 
-}  // namespace piton
+// One new query per (batch, head) against keys 0 .. n_keys-1 of a cache (the decode step of a
+// KV-cached decoder): one wavefront per (batch, head); lanes score keys j = lane, lane + 64, ...
+// into LDS, two DPP reductions give the max and the sum, then lane d accumulates
+// sum_j p_j V[j][d] with coalesced V rows.
+constexpr int kMaxDecodeKeys = 8192;
 
-extern "C" int32_t piton_mi355x_attn_fwd(const float *q, const float *k, const float *v, float *out, float sm_scale,
-                                         int64_t stride_qh, int64_t stride_qm, int64_t stride_kh, int64_t stride_kn,
-                                         int64_t stride_kk, int64_t stride_vh, int64_t stride_vn, int64_t stride_oh,
-                                         int64_t stride_om, int64_t n_ctx, int64_t n_heads, int32_t head_dim,
-                                         int32_t causal, void *stream) {
-    using namespace piton;
-    PITON_REQUIRE(n_ctx >= 0 && n_heads >= 0, PITON_EINVAL, "attn_fwd: negative N_CTX or heads");
-    PITON_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, PITON_EUNSUPPORTED,
-                  "attn_fwd: HEAD_DIM %d not in {16, 32, 64, 128}", head_dim);
-    PITON_REQUIRE(n_ctx == 0 || n_heads == 0 || (q && k && v && out), PITON_EINVAL, "attn_fwd: null pointer");
-    PITON_REQUIRE(aligned4(q) && aligned4(k) && aligned4(v) && aligned4(out), PITON_EINVAL,
-                  "attn_fwd: pointers must be 4-byte aligned");
-    PITON_REQUIRE(n_heads <= 65535, PITON_EUNSUPPORTED, "attn_fwd: %lld heads exceed grid axis 1", (long long)n_heads);
-    PITON_REQUIRE(n_ctx < (1LL << 31) - 64, PITON_EUNSUPPORTED, "attn_fwd: N_CTX %lld too large", (long long)n_ctx);
-    int rc = require_device();
-    if (rc) return rc;
-    if (n_ctx == 0 || n_heads == 0) return PITON_OK;
+struct DecodeArgs {
+    const float *q, *k, *v;
+    float *o;
+    float scale;  // sm_scale * log2(e)
+    int64_t s_qb, s_qh, s_kb, s_kh, s_kn, s_vb, s_vh, s_vn, s_ob, s_oh;
+    int n_keys, n_heads, head_dim;
+};
 
-    AttnArgs g{q, k, v, out, sm_scale * 1.44269504088896341f, stride_qh, stride_qm, stride_kh, stride_kn, stride_kk,
-               stride_vh, stride_vn, stride_oh, stride_om, n_ctx, head_dim, causal ? 1 : 0, 0};
-    g.v_vec = aligned16(v) && stride_vn % 4 == 0 && stride_vh % 4 == 0 && head_dim % 4 == 0;
+template <int D>
+__global__ __launch_bounds__(64) void attn_decode_kernel(DecodeArgs g) {
+    __shared__ float p[kMaxDecodeKeys];
+    const int lane = threadIdx.x;
+    const int64_t bh = blockIdx.x, b = bh / g.n_heads, h = bh % g.n_heads;
+    const float *qp = g.q + b * g.s_qb + h * g.s_qh;
+    const float *kp = g.k + b * g.s_kb + h * g.s_kh;
+    const float *vp = g.v + b * g.s_vb + h * g.s_vh;
+    float q[D];
+#pragma unroll
+    for (int d = 0; d < D; d++) q[d] = d < g.head_dim ? qp[d] * g.scale : 0.f;
+    float mloc = -INFINITY;
+    for (int j = lane; j < g.n_keys; j += 64) {
+        const float *kr = kp + (int64_t)j * g.s_kn;
+        float s = 0.f;
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (d < g.head_dim) s = fmaf(q[d], kr[d], s);
+        p[j] = s;
+        mloc = fmaxf(mloc, s);
+    }
+    const float m = wave_reduce(mloc, MaxOp());
+    float lsum = 0.f;
+    for (int j = lane; j < g.n_keys; j += 64) {
+        const float e = __builtin_amdgcn_exp2f(p[j] - m);
+        p[j] = e;
+        lsum += e;
+    }
+    const float inv = 1.0f / wave_reduce(lsum, SumOp());
+    __syncthreads();
+    float *op = g.o + b * g.s_ob + h * g.s_oh;
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += 64) {
+        const int d = d0 + lane;
+        if (d < g.head_dim) {
+            float acc = 0.f;
+            for (int j = 0; j < g.n_keys; j++) acc = fmaf(p[j], vp[(int64_t)j * g.s_vn + d], acc);
+            op[d] = acc * inv;
+        }
+    }
+}
+
+static int attn_launch(AttnArgs g, int64_t batch, int64_t n_heads, int32_t head_dim, hipStream_t st) {
+    g.v_vec = aligned16(g.v) && g.s_vn % 4 == 0 && g.s_vh % 4 == 0 && g.s_vb % 4 == 0 && head_dim % 4 == 0;
     int kl = K_SCALAR;
-    if (stride_kk == 1 && stride_kn % 4 == 0 && stride_kh % 4 == 0 && aligned16(k) && head_dim % 4 == 0) kl = K_VEC_D;
-    else if (stride_kn == 1 && stride_kk % 4 == 0 && stride_kh % 4 == 0 && aligned16(k) && n_ctx % 4 == 0) kl = K_VEC_N;
-    const dim3 grid((unsigned)((n_ctx + ABM - 1) / ABM), (unsigned)n_heads);
-    hipStream_t st = (hipStream_t)stream;
+    if (g.s_kk == 1 && g.s_kn % 4 == 0 && g.s_kh % 4 == 0 && g.s_kb % 4 == 0 && aligned16(g.k) && head_dim % 4 == 0)
+        kl = K_VEC_D;
+    else if (g.s_kn == 1 && g.s_kk % 4 == 0 && g.s_kh % 4 == 0 && g.s_kb % 4 == 0 && aligned16(g.k) && g.n_ctx % 4 == 0)
+        kl = K_VEC_N;
+    const dim3 grid((unsigned)((g.n_ctx + ABM - 1) / ABM), (unsigned)(batch * n_heads));
     if (head_dim <= 32) launch_d<32>(kl, g, grid, st);
     else if (head_dim == 64) launch_d<64>(kl, g, grid, st);
     else launch_d<128>(kl, g, grid, st);
-    rc = check_launch("attn_fwd");
+    return check_launch("attn_fwd");
+}
+
+static int attn_check(const float *q, const float *k, const float *v, const float *out, int64_t n_ctx, int64_t batch,
+                      int64_t n_heads, int32_t head_dim) {
+    PITON_REQUIRE(n_ctx >= 0 && n_heads >= 0 && batch >= 0, PITON_EINVAL, "attn_fwd: negative N_CTX, batch or heads");
+    PITON_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, PITON_EUNSUPPORTED,
+                  "attn_fwd: HEAD_DIM %d not in {16, 32, 64, 128}", head_dim);
+    PITON_REQUIRE(n_ctx == 0 || n_heads == 0 || batch == 0 || (q && k && v && out), PITON_EINVAL,
+                  "attn_fwd: null pointer");
+    PITON_REQUIRE(aligned4(q) && aligned4(k) && aligned4(v) && aligned4(out), PITON_EINVAL,
+                  "attn_fwd: pointers must be 4-byte aligned");
+    PITON_REQUIRE(batch * n_heads <= 65535, PITON_EUNSUPPORTED, "attn_fwd: %lld heads exceed grid axis 1",
+                  (long long)(batch * n_heads));
+    PITON_REQUIRE(n_ctx < (1LL << 31) - 64, PITON_EUNSUPPORTED, "attn_fwd: N_CTX %lld too large", (long long)n_ctx);
+    return PITON_OK;
+}
+
+}  // namespace piton
+
+extern "C" {
+
+int32_t piton_mi355x_attn_fwd(const float *q, const float *k, const float *v, float *out, float sm_scale,
+                              int64_t stride_qh, int64_t stride_qm, int64_t stride_kh, int64_t stride_kn,
+                              int64_t stride_kk, int64_t stride_vh, int64_t stride_vn, int64_t stride_oh,
+                              int64_t stride_om, int64_t n_ctx, int64_t n_heads, int32_t head_dim, int32_t causal,
+                              void *stream) {
+    using namespace piton;
+    int rc = attn_check(q, k, v, out, n_ctx, 1, n_heads, head_dim);
+    if (rc) return rc;
+    rc = require_device();
+    if (rc) return rc;
+    if (n_ctx == 0 || n_heads == 0) return PITON_OK;
+    AttnArgs g{q, k, v, out, sm_scale * 1.44269504088896341f, stride_qh, stride_qm, stride_kh, stride_kn, stride_kk,
+               stride_vh, stride_vn, stride_oh, stride_om, n_ctx, 0, 0, 0, 0, n_heads, head_dim, causal ? 1 : 0, 0};
+    rc = attn_launch(g, 1, n_heads, head_dim, (hipStream_t)stream);
     if (rc == PITON_OK) clear_error();
     return rc;
 }
+
+int32_t piton_mi355x_attn_fwd_batched(const float *q, const float *k, const float *v, float *out, float sm_scale,
+                                      int64_t stride_qb, int64_t stride_qh, int64_t stride_qm, int64_t stride_kb,
+                                      int64_t stride_kh, int64_t stride_kn, int64_t stride_kk, int64_t stride_vb,
+                                      int64_t stride_vh, int64_t stride_vn, int64_t stride_ob, int64_t stride_oh,
+                                      int64_t stride_om, int64_t n_ctx, int64_t batch, int64_t n_heads,
+                                      int32_t head_dim, int32_t causal, void *stream) {
+    using namespace piton;
+    int rc = attn_check(q, k, v, out, n_ctx, batch, n_heads, head_dim);
+    if (rc) return rc;
+    rc = require_device();
+    if (rc) return rc;
+    if (n_ctx == 0 || n_heads == 0 || batch == 0) return PITON_OK;
+    AttnArgs g{q, k, v, out, sm_scale * 1.44269504088896341f, stride_qh, stride_qm, stride_kh, stride_kn, stride_kk,
+               stride_vh, stride_vn, stride_oh, stride_om, n_ctx, stride_qb, stride_kb, stride_vb, stride_ob, n_heads,
+               head_dim, causal ? 1 : 0, 0};
+    rc = attn_launch(g, batch, n_heads, head_dim, (hipStream_t)stream);
+    if (rc == PITON_OK) clear_error();
+    return rc;
+}
+
+int32_t piton_mi355x_attn_decode(const float *q, const float *k, const float *v, float *out, float sm_scale,
+                                 int64_t stride_qb, int64_t stride_qh, int64_t stride_kb, int64_t stride_kh,
+                                 int64_t stride_kn, int64_t stride_vb, int64_t stride_vh, int64_t stride_vn,
+                                 int64_t stride_ob, int64_t stride_oh, int64_t n_keys, int64_t batch, int64_t n_heads,
+                                 int32_t head_dim, void *stream) {
+    using namespace piton;
+    PITON_REQUIRE(n_keys >= 1 && batch >= 0 && n_heads >= 0, PITON_EINVAL, "attn_decode: n_keys=%lld batch=%lld",
+                  (long long)n_keys, (long long)batch);
+    PITON_REQUIRE(n_keys <= kMaxDecodeKeys, PITON_EUNSUPPORTED, "attn_decode: %lld keys exceed %d",
+                  (long long)n_keys, kMaxDecodeKeys);
+    PITON_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, PITON_EUNSUPPORTED,
+                  "attn_decode: HEAD_DIM %d not in {16, 32, 64, 128}", head_dim);
+    PITON_REQUIRE(batch * n_heads == 0 || (q && k && v && out), PITON_EINVAL, "attn_decode: null pointer");
+    PITON_REQUIRE(batch * n_heads <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "attn_decode: too many heads");
+    int rc = require_device();
+    if (rc) return rc;
+    if (batch * n_heads == 0) return PITON_OK;
+    DecodeArgs g{q, k, v, out, sm_scale * 1.44269504088896341f, stride_qb, stride_qh, stride_kb, stride_kh, stride_kn,
+                 stride_vb, stride_vh, stride_vn, stride_ob, stride_oh, (int)n_keys, (int)n_heads, head_dim};
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 grid((unsigned)(batch * n_heads)), block(64);
+    if (head_dim <= 32) hipLaunchKernelGGL(attn_decode_kernel<32>, grid, block, 0, st, g);
+    else if (head_dim == 64) hipLaunchKernelGGL(attn_decode_kernel<64>, grid, block, 0, st, g);
+    else hipLaunchKernelGGL(attn_decode_kernel<128>, grid, block, 0, st, g);
+    rc = check_launch("attn_decode");
+    if (rc == PITON_OK) clear_error();
+    return rc;
+}
+
+}  // extern "C"

@@ -70,20 +70,21 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const float *x, flo
     }
 }
 
-// out[b, t, :] = tok[ids[b, t], :] + pos[pos_offset + t, :]
-__global__ __launch_bounds__(256) void embedding_kernel(const int32_t *ids, int64_t ids_ld, const float *tok,
-                                                        const float *pos, float *out, int64_t T, int64_t d,
-                                                        int64_t vocab, int64_t pos_offset, int64_t total,
-                                                        int32_t *err) {
+// out[b, t, :] = tok[ids[b, t], :] + pos[pos_offset + t, :] through element strides
+__global__ __launch_bounds__(256) void embedding_kernel(const int32_t *ids, int64_t ids_sb, int64_t ids_st,
+                                                        const float *tok, const float *pos, float *out, int64_t out_sb,
+                                                        int64_t out_st, int64_t T, int64_t d, int64_t vocab,
+                                                        int64_t pos_offset, int64_t total, int32_t *err) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
         const int64_t bt = i / d, c = i % d;
         const int64_t b = bt / T, t = bt % T;
-        const int32_t id = ids[b * ids_ld + t];
+        const int32_t id = ids[b * ids_sb + t * ids_st];
+        float *o = out + b * out_sb + t * out_st + c;
         if (id < 0 || id >= vocab) {
-            out[i] = __int_as_float(0x7FC00000);
+            *o = __int_as_float(0x7FC00000);
             if (err) *err = 1;
         } else {
-            out[i] = tok[(int64_t)id * d + c] + pos[(pos_offset + t) * d + c];
+            *o = tok[(int64_t)id * d + c] + pos[(pos_offset + t) * d + c];
         }
     }
 }
@@ -147,21 +148,20 @@ int32_t piton_mi355x_layernorm(const float *x, float *out, int64_t n, float eps,
     return rc;
 }
 
-int32_t piton_mi355x_embedding(const int32_t *ids, int64_t ids_ld, const float *tok, const float *pos, float *out,
-                               int64_t batch, int64_t T, int64_t d_model, int64_t vocab, int64_t pos_offset,
-                               int32_t *err_flag, void *stream) {
+int32_t piton_mi355x_embedding(const int32_t *ids, int64_t ids_sb, int64_t ids_st, const float *tok, const float *pos,
+                               float *out, int64_t out_sb, int64_t out_st, int64_t batch, int64_t T, int64_t d_model,
+                               int64_t vocab, int64_t pos_offset, int32_t *err_flag, void *stream) {
     using namespace piton;
-    PITON_REQUIRE(batch >= 0 && T >= 0 && d_model >= 1 && vocab >= 1 && pos_offset >= 0 && ids_ld >= T, PITON_EINVAL,
-                  "embedding: batch=%lld T=%lld d_model=%lld vocab=%lld pos_offset=%lld ids_ld=%lld",
-                  (long long)batch, (long long)T, (long long)d_model, (long long)vocab, (long long)pos_offset,
-                  (long long)ids_ld);
+    PITON_REQUIRE(batch >= 0 && T >= 0 && d_model >= 1 && vocab >= 1 && pos_offset >= 0, PITON_EINVAL,
+                  "embedding: batch=%lld T=%lld d_model=%lld vocab=%lld pos_offset=%lld", (long long)batch,
+                  (long long)T, (long long)d_model, (long long)vocab, (long long)pos_offset);
     PITON_REQUIRE(batch * T == 0 || (ids && tok && pos && out), PITON_EINVAL, "embedding: null pointer");
     int rc = require_device();
     if (rc) return rc;
     const int64_t total = batch * T * d_model;
     if (total == 0) return PITON_OK;
-    hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, ids, ids_ld, tok,
-                       pos, out, T, d_model, vocab, pos_offset, total, err_flag);
+    hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, ids, ids_sb, ids_st,
+                       tok, pos, out, out_sb, out_st, T, d_model, vocab, pos_offset, total, err_flag);
     rc = check_launch("embedding");
     if (rc == PITON_OK) clear_error();
     return rc;

@@ -37,6 +37,8 @@ struct GemmArgs {
     int group_m;
     const float *bias;  // dense epilogue (nullable)
     int relu;
+    const float *res;   // residual added after bias / ReLU (nullable), element (m, n) at m*s_rm + n
+    int64_t s_rm;
     int a_kfast, b_nfast;  // scalar loaders: which index runs fastest across threads
 };
 
@@ -240,6 +242,7 @@ __global__ __launch_bounds__(GTHREADS) void gemm_f32_kernel(GemmArgs g) {
                     float v = acc[mb][nb][r];
                     if (g.bias) v += bias;
                     if (g.relu && v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
+                    if (g.res) v += g.res[row * g.s_rm + col];
                     g.c[row * g.s_cm + col * g.s_cn] = v;
                 }
             }
@@ -312,7 +315,7 @@ int32_t piton_mi355x_matmul(const float *a, const float *b, float *c, int64_t M,
     int rc = require_device();
     if (rc) return rc;
     GemmArgs g{a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn,
-               group_size_m, nullptr, 0, 0, 0};
+               group_size_m, nullptr, 0, nullptr, 0, 0, 0};
     rc = launch_gemm(g, (hipStream_t)stream, "matmul");
     if (rc == PITON_OK) clear_error();
     return rc;
@@ -333,7 +336,7 @@ int32_t piton_mi355x_dense(const float *x, const float *w, const float *bias, fl
     int rc = require_device();
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
-    GemmArgs g{x, w, y, M, N, K, K, 1, N, 1, N, 1, 1, add_bias ? bias : nullptr, relu ? 1 : 0, 0, 0};
+    GemmArgs g{x, w, y, M, N, K, K, 1, N, 1, N, 1, 1, add_bias ? bias : nullptr, relu ? 1 : 0, nullptr, 0, 0, 0};
     rc = launch_gemm(g, st, "dense");
     if (rc) return rc;
     if (argmax_out && M > 0) {
@@ -344,6 +347,26 @@ int32_t piton_mi355x_dense(const float *x, const float *w, const float *bias, fl
     }
     clear_error();
     return PITON_OK;
+}
+
+int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *w, const float *bias, const float *residual,
+                            int64_t ldr, float *y, int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t relu,
+                            void *stream) {
+    using namespace piton;
+    PITON_REQUIRE(M >= 0 && N > 0 && K > 0, PITON_EINVAL, "linear: bad size M=%lld N=%lld K=%lld", (long long)M,
+                  (long long)N, (long long)K);
+    PITON_REQUIRE(ldx >= K && ldy >= N && (!residual || ldr >= N), PITON_EINVAL,
+                  "linear: row strides (%lld, %lld, %lld) shorter than the rows", (long long)ldx, (long long)ldy,
+                  (long long)ldr);
+    PITON_REQUIRE(M == 0 || (x && w && y), PITON_EINVAL, "linear: null X, W or Y");
+    PITON_REQUIRE(aligned4(x) && aligned4(w) && aligned4(y) && aligned4(bias) && aligned4(residual), PITON_EINVAL,
+                  "linear: pointers must be 4-byte aligned");
+    int rc = require_device();
+    if (rc) return rc;
+    GemmArgs g{x, w, y, M, N, K, ldx, 1, N, 1, ldy, 1, 1, bias, relu ? 1 : 0, residual, ldr, 0, 0};
+    rc = launch_gemm(g, (hipStream_t)stream, "linear");
+    if (rc == PITON_OK) clear_error();
+    return rc;
 }
 
 int32_t piton_mi355x_argmax_rows(const float *x, int64_t rows, int64_t ld, int64_t n, int32_t *out, void *stream) {

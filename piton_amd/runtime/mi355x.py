@@ -50,7 +50,10 @@ SIGNATURES = {
     "piton_mi355x_add": [_p, _p, _p, _i64, _p],
     "piton_mi355x_layernorm": [_p, _p, _i64, _f32, _i64, _i64, _p],
     "piton_mi355x_argmax_rows": [_p, _i64, _i64, _i64, _p, _p],
-    "piton_mi355x_embedding": [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p],
+    "piton_mi355x_embedding": [_p, _i64, _i64, _p, _p, _p] + [_i64] * 7 + [_p, _p],
+    "piton_mi355x_linear": [_p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p],
+    "piton_mi355x_attn_fwd_batched": [_p, _p, _p, _p, _f32] + [_i64] * 16 + [_i32, _i32, _p],
+    "piton_mi355x_attn_decode": [_p, _p, _p, _p, _f32] + [_i64] * 13 + [_i32, _p],
 }
 
 
@@ -219,11 +222,47 @@ def argmax_rows(x, rows, ld, n, out):
     _call("piton_mi355x_argmax_rows", _ptr(x), rows, ld, n, _ptr(out), _stream())
 
 
-def embedding(ids, ids_ld, tok, pos, out, batch, T, d_model, vocab, pos_offset, err_flag=None):
-    check_tensor("ids", ids, dtype=torch.int32, max_offset=_span((batch, ids_ld), (T, 1)))
+def embedding(ids, ids_sb, ids_st, tok, pos, out, out_sb, out_st, batch, T, d_model, vocab, pos_offset,
+              err_flag=None):
+    """out[b, t, :] = tok[ids[b, t]] + pos[pos_offset + t] through element strides."""
+    check_tensor("ids", ids, dtype=torch.int32, max_offset=_span((batch, ids_sb), (T, ids_st)))
     check_tensor("tok", tok, max_offset=vocab * d_model - 1)
     check_tensor("pos", pos, max_offset=(pos_offset + T) * d_model - 1)
-    check_tensor("out", out, max_offset=batch * T * d_model - 1)
+    check_tensor("out", out, max_offset=_span((batch, out_sb), (T, out_st), (d_model, 1)))
     check_tensor("err_flag", err_flag, dtype=torch.int32, max_offset=0, allow_none=True)
-    _call("piton_mi355x_embedding", _ptr(ids), ids_ld, _ptr(tok), _ptr(pos), _ptr(out), batch, T, d_model, vocab,
-          pos_offset, _ptr(err_flag), _stream())
+    _call("piton_mi355x_embedding", _ptr(ids), ids_sb, ids_st, _ptr(tok), _ptr(pos), _ptr(out), out_sb, out_st, batch,
+          T, d_model, vocab, pos_offset, _ptr(err_flag), _stream())
+
+
+def linear(x, ldx, w, bias, residual, ldr, y, ldy, M, N, K, relu=False):
+    """Y = [ReLU](X W [+ b]) [+ R] over strided rows (the decoder's projections)."""
+    check_tensor("x", x, max_offset=_span((M, ldx), (K, 1)))
+    check_tensor("w", w, max_offset=K * N - 1)
+    check_tensor("bias", bias, max_offset=N - 1, allow_none=True)
+    check_tensor("residual", residual, max_offset=_span((M, ldr), (N, 1)), allow_none=True)
+    check_tensor("y", y, max_offset=_span((M, ldy), (N, 1)))
+    _call("piton_mi355x_linear", _ptr(x), ldx, _ptr(w), _ptr(bias), _ptr(residual), ldr, _ptr(y), ldy, M, N, K,
+          int(bool(relu)), _stream())
+
+
+def attn_fwd_batched(q, k, v, out, sm_scale, s_qb, s_qh, s_qm, s_kb, s_kh, s_kn, s_kk, s_vb, s_vh, s_vn, s_ob, s_oh,
+                     s_om, n_ctx, batch, heads, head_dim, causal):
+    """attn_fwd_kernel over batch x heads."""
+    check_tensor("Q", q, max_offset=_span((batch, s_qb), (heads, s_qh), (n_ctx, s_qm), (head_dim, 1)))
+    check_tensor("K", k, max_offset=_span((batch, s_kb), (heads, s_kh), (n_ctx, s_kn), (head_dim, s_kk)))
+    check_tensor("V", v, max_offset=_span((batch, s_vb), (heads, s_vh), (n_ctx, s_vn), (head_dim, 1)))
+    check_tensor("Out", out, max_offset=_span((batch, s_ob), (heads, s_oh), (n_ctx, s_om), (head_dim, 1)))
+    _call("piton_mi355x_attn_fwd_batched", _ptr(q), _ptr(k), _ptr(v), _ptr(out), float(sm_scale), s_qb, s_qh, s_qm,
+          s_kb, s_kh, s_kn, s_kk, s_vb, s_vh, s_vn, s_ob, s_oh, s_om, n_ctx, batch, heads, int(head_dim),
+          int(bool(causal)), _stream())
+
+
+def attn_decode(q, k, v, out, sm_scale, s_qb, s_qh, s_kb, s_kh, s_kn, s_vb, s_vh, s_vn, s_ob, s_oh, n_keys, batch,
+                heads, head_dim):
+    """One query per (batch, head) against n_keys cached keys."""
+    check_tensor("q", q, max_offset=_span((batch, s_qb), (heads, s_qh), (head_dim, 1)))
+    check_tensor("k", k, max_offset=_span((batch, s_kb), (heads, s_kh), (n_keys, s_kn), (head_dim, 1)))
+    check_tensor("v", v, max_offset=_span((batch, s_vb), (heads, s_vh), (n_keys, s_vn), (head_dim, 1)))
+    check_tensor("out", out, max_offset=_span((batch, s_ob), (heads, s_oh), (head_dim, 1)))
+    _call("piton_mi355x_attn_decode", _ptr(q), _ptr(k), _ptr(v), _ptr(out), float(sm_scale), s_qb, s_qh, s_kb, s_kh,
+          s_kn, s_vb, s_vh, s_vn, s_ob, s_oh, n_keys, batch, heads, int(head_dim), _stream())

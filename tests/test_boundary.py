@@ -36,6 +36,34 @@ def test_library_exports_every_declared_entry():
     assert lib.piton_mi355x_abi_version() == mi355x.ABI_VERSION
 
 
+def header_prototypes():
+    """entry name -> list of parameter C types, parsed from include/*.h."""
+    protos = {}
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        for name, params in re.findall(r"PITON_API\s+[\w\s\*]+?\b(piton_mi355x_\w+)\s*\(([^)]*)\)", text):
+            params = " ".join(params.split())
+            protos[name] = [] if params == "void" else [p.strip() for p in params.split(",")]
+    return protos
+
+
+def _ctype_of(decl: str):
+    decl = decl.replace("const ", "")
+    if "*" in decl:
+        return "ptr"
+    t = decl.split()[0]
+    return {"int64_t": "i64", "int32_t": "i32", "float": "f32"}[t]
+
+
+def test_ctypes_signatures_match_the_header():
+    protos = header_prototypes()
+    names = {ctypes.c_void_p: "ptr", ctypes.c_int64: "i64", ctypes.c_int32: "i32", ctypes.c_float: "f32"}
+    for entry, argtypes in mi355x.SIGNATURES.items():
+        want = [_ctype_of(p) for p in protos[entry]]
+        got = [names.get(a, "ptr") for a in argtypes]
+        assert got == want, entry
+
+
 def _raw():
     return mi355x.lib()
 

@@ -1,0 +1,133 @@
+"""The TinyGPT decoder (piton_amd/tinygpt.py) on the MI355X against its float64 oracle
+(oracle/tinygpt64.py).
+
+The reference has no decoder, so parity is against the build's own float64 model (parity of
+the composition itself is unpinned). Bar: every piece within float32 tolerance of float64; the
+greedy token ids equal the oracle's, except that a sequence may diverge at a step whose float64
+top-2 logit margin is below TAU (a near-tie that float32 cannot resolve); each such divergence
+is reported with its margin."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp64, tinygpt64
+from piton_amd import tinygpt
+from piton_amd.runtime import mi355x as rt
+
+pytestmark = pytest.mark.gpu
+TAU = 1e-4  # float32 logits of this model carry ~1e-6 absolute error; margins below TAU are ties
+
+
+def test_linear_residual_relu_strided():
+    rng = np.random.default_rng(0)
+    M, N, K = 70, 96, 48
+    x = rng.standard_normal((M, K + 5)).astype(np.float32)
+    w = rng.standard_normal((K, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    r = rng.standard_normal((M, N + 3)).astype(np.float32)
+    tx, tw, tb, tr = (torch.from_numpy(t).cuda() for t in (x, w, b, r))
+    y = torch.full((M, N + 7), -2.0, device="cuda")
+    rt.linear(tx, K + 5, tw, tb, tr, N + 3, y, N + 7, M, N, K, relu=True)
+    torch.cuda.synchronize()
+    ref = np.maximum(x[:, :K].astype(np.float64) @ w + b, 0) + r[:, :N]
+    got = y.cpu().numpy()
+    assert fp64.rel_fro(got[:, :N], ref) <= 1e-6
+    assert (got[:, N:] == -2.0).all()
+    # in place: y is the residual
+    y2 = tr.clone()
+    rt.linear(tx, K + 5, tw, None, y2, N + 3, y2, N + 3, M, N, K)
+    torch.cuda.synchronize()
+    ref2 = x[:, :K].astype(np.float64) @ w + r[:, :N]
+    assert fp64.rel_fro(y2.cpu().numpy()[:, :N], ref2) <= 1e-6
+
+
+def test_position_major_attention_prefill_and_decode():
+    """The decoder's layout: qkv rows t*B + b of 3*D; heads through strides."""
+    rng = np.random.default_rng(1)
+    B, T, H, Dh = 5, 40, 4, 64
+    D = H * Dh
+    qkv = rng.standard_normal((T * B, 3 * D)).astype(np.float32)
+    t = torch.from_numpy(qkv).cuda()
+    att = torch.zeros((T * B, D), device="cuda")
+    scale = 1 / 8
+    rt.attn_fwd_batched(t, t[:, D:], t[:, 2 * D:], att, scale, 3 * D, Dh, B * 3 * D, 3 * D, Dh, B * 3 * D, 1, 3 * D, Dh,
+                        B * 3 * D, D, Dh, B * D, T, B, H, Dh, True)
+    dec = torch.zeros((B, D), device="cuda")
+    rt.attn_decode(t[(T - 1) * B:], t[:, D:], t[:, 2 * D:], dec, scale, 3 * D, Dh, 3 * D, Dh, B * 3 * D, 3 * D, Dh,
+                   B * 3 * D, D, Dh, T, B, H, Dh)
+    torch.cuda.synchronize()
+    x = qkv.reshape(T, B, 3, H, Dh).transpose(2, 1, 3, 0, 4)  # [3, B, H, T, Dh]
+    ref = fp64.attention_reference(x[0], x[1], x[2], True, scale)       # [B, H, T, Dh]
+    got = att.cpu().numpy().reshape(T, B, H, Dh).transpose(1, 2, 0, 3)
+    assert fp64.rel_fro(got, ref) <= 1e-5
+    got_dec = dec.cpu().numpy().reshape(B, H, Dh)
+    assert fp64.rel_fro(got_dec, ref[:, :, -1]) <= 1e-5
+
+
+def test_strided_embedding_and_bad_ids():
+    rng = np.random.default_rng(2)
+    B, T, D, V = 3, 7, 16, 11
+    tok = torch.from_numpy(rng.standard_normal((V, D)).astype(np.float32)).cuda()
+    pos = torch.from_numpy(rng.standard_normal((20, D)).astype(np.float32)).cuda()
+    ids_np = rng.integers(0, V, (T, B)).astype(np.int32)  # position-major
+    ids = torch.from_numpy(ids_np.reshape(-1)).cuda()
+    out = torch.zeros((T * B, D), device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rt.embedding(ids, 1, B, tok, pos[2:], out, D, B * D, B, T, D, V, 0, err)
+    torch.cuda.synchronize()
+    want = tok.cpu().numpy()[ids_np] + pos.cpu().numpy()[2:2 + T][:, None]
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(T, B, D), want)
+    assert int(err.item()) == 0
+    ids[4] = V  # out of the vocabulary: NaN row and the flag
+    rt.embedding(ids, 1, B, tok, pos, out, D, B * D, B, T, D, V, 0, err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1 and np.isnan(out.cpu().numpy()[4]).all()
+
+
+def test_prefill_logits_match_float64():
+    w = tinygpt.init_weights(seed=0)
+    prompts = tinygpt.seeded_prompts(batch=8, length=32)
+    model = tinygpt.TinyGPT(w, batch=8)
+    model.generate(prompts, 1)
+    got = model.last_logits()
+    # float64 logits of the same prefix
+    _, margins = tinygpt64.generate(w, prompts, 1)
+    d = {k: np.asarray(v, np.float64) for k, v in w.items()}
+    x = d["tok"][prompts] + d["pos"][:32][None]
+    for i in range(4):
+        h = tinygpt64.layernorm(x, 1e-5)
+        qkv = h @ d[f"wqkv{i}"]
+        q, k, v = (qkv[..., j * 256:(j + 1) * 256].reshape(8, 32, 4, 64).transpose(0, 2, 1, 3) for j in range(3))
+        a = fp64.attention_reference(q, k, v, True, 1 / 8).transpose(0, 2, 1, 3).reshape(8, 32, 256)
+        x = x + a @ d[f"wo{i}"]
+        x = x + np.maximum(tinygpt64.layernorm(x, 1e-5) @ d[f"w1{i}"], 0) @ d[f"w2{i}"]
+    ref = tinygpt64.layernorm(x[:, -1], 1e-5) @ d["lm"]
+    assert fp64.rel_fro(got, ref) <= 1e-5
+
+
+def test_kv_cache_decode_equals_recompute():
+    w = tinygpt.init_weights(seed=0)
+    prompts = tinygpt.seeded_prompts(batch=8, length=32, seed=5)
+    model = tinygpt.TinyGPT(w, batch=8)
+    a = model.generate(prompts, 24, kv_cache=True)
+    b = model.generate(prompts, 24, kv_cache=False)
+    want, margins = tinygpt64.generate(w, prompts, 24)
+    for got in (a, b):
+        for seq, pos, margin in tinygpt64.first_divergence(got, want, margins, 32):
+            assert margin < TAU, (seq, pos, margin)
+    np.testing.assert_array_equal(a[:, :32], prompts)
+
+
+def test_config_greedy_64x128_matches_float64():
+    """Config: 4 layers, d_model 256, 4 heads, MLP 1024, vocab 256, context 256, init
+    N(0, 0.02); 64 seeded prompts of 32 tokens, 128 greedy tokens each."""
+    w = tinygpt.init_weights(seed=0)
+    prompts = tinygpt.seeded_prompts(batch=64, length=32)
+    model = tinygpt.TinyGPT(w, batch=64)
+    got = model.generate(prompts, 128)
+    want, margins = tinygpt64.generate(w, prompts, 128)
+    div = tinygpt64.first_divergence(got, want, margins, 32)
+    print(f"\ntoken ids equal in {64 - len(div)} of 64 sequences; divergences (seq, pos, fp64 margin): {div}")
+    for seq, pos, margin in div:
+        assert margin < TAU, (seq, pos, margin)
+    assert len(div) <= 2

@@ -1,0 +1,88 @@
+"""The decoder driver's memory layout on the host: piton_amd/tinygpt.py runs against a host
+mirror of the C ABI entries it calls (each reads and writes memory through exactly the
+pointers and element strides the driver passes), and must decode the same tokens as the
+float64 oracle. A wrong offset or stride in the driver fails here without a GPU."""
+import numpy as np
+import torch
+
+from oracle import tinygpt64
+from piton_amd import tinygpt
+
+
+def view(t, size, stride):
+    return torch.as_strided(t, size, stride, storage_offset=t.storage_offset())
+
+
+class HostABI:
+    """Float64 mirror of the entries the decoder uses, addressing memory as the C ABI does."""
+
+    @staticmethod
+    def embedding(ids, ids_sb, ids_st, tok, pos, out, out_sb, out_st, batch, T, d, vocab, pos_offset, err=None):
+        i = view(ids, (batch, T), (ids_sb, ids_st)).long()
+        o = view(out, (batch, T, d), (out_sb, out_st, 1))
+        o.copy_(tok[i] + pos[pos_offset:pos_offset + T][None])
+
+    @staticmethod
+    def layernorm(x, out, n, eps, rows, rs):
+        xv = view(x, (rows, n), (rs, 1)).double()
+        d = xv - xv.mean(1, keepdim=True)
+        view(out, (rows, n), (rs, 1)).copy_(d / torch.sqrt((d * d).mean(1, keepdim=True) + eps))
+
+    @staticmethod
+    def linear(x, ldx, w, bias, residual, ldr, y, ldy, M, N, K, relu=False):
+        r = view(x, (M, K), (ldx, 1)).double() @ w.double()
+        if bias is not None:
+            r = r + bias.double()
+        if relu:
+            r = torch.clamp(r, min=0)
+        if residual is not None:
+            r = r + view(residual, (M, N), (ldr, 1)).double()
+        view(y, (M, N), (ldy, 1)).copy_(r)
+
+    @staticmethod
+    def attn_fwd_batched(q, k, v, out, scale, s_qb, s_qh, s_qm, s_kb, s_kh, s_kn, s_kk, s_vb, s_vh, s_vn, s_ob,
+                         s_oh, s_om, n, batch, heads, dh, causal):
+        Q = view(q, (batch, heads, n, dh), (s_qb, s_qh, s_qm, 1)).double()
+        Kt = view(k, (batch, heads, n, dh), (s_kb, s_kh, s_kn, s_kk)).double()
+        V = view(v, (batch, heads, n, dh), (s_vb, s_vh, s_vn, 1)).double()
+        s = Q @ Kt.transpose(-1, -2) * scale
+        if causal:
+            s = s.masked_fill(torch.triu(torch.ones(n, n, dtype=torch.bool), 1), float("-inf"))
+        view(out, (batch, heads, n, dh), (s_ob, s_oh, s_om, 1)).copy_(torch.softmax(s, -1) @ V)
+
+    @staticmethod
+    def attn_decode(q, k, v, out, scale, s_qb, s_qh, s_kb, s_kh, s_kn, s_vb, s_vh, s_vn, s_ob, s_oh, n_keys, batch,
+                    heads, dh):
+        Q = view(q, (batch, heads, 1, dh), (s_qb, s_qh, 0, 1)).double()
+        Kt = view(k, (batch, heads, n_keys, dh), (s_kb, s_kh, s_kn, 1)).double()
+        V = view(v, (batch, heads, n_keys, dh), (s_vb, s_vh, s_vn, 1)).double()
+        p = torch.softmax(Q @ Kt.transpose(-1, -2) * scale, -1)
+        view(out, (batch, heads, dh), (s_ob, s_oh, 1)).copy_((p @ V)[:, :, 0])
+
+    @staticmethod
+    def argmax_rows(x, rows, ld, n, out):
+        out[:rows].copy_(torch.argmax(view(x, (rows, n), (ld, 1)), 1).int())
+
+
+def run_host(monkeypatch, kv_cache, steps=6, batch=3):
+    cfg = tinygpt.Config(d_model=64, n_heads=2, d_mlp=96, vocab=29, context=24, n_layers=2)
+    w = tinygpt.init_weights(cfg, seed=1)
+    w = {k: (v * 10 if k.startswith("w") or k == "lm" else v) for k, v in w.items()}  # wide margins
+    prompts = tinygpt.seeded_prompts(batch=batch, length=5, vocab=cfg.vocab, seed=2)
+    monkeypatch.setattr(tinygpt, "rt", HostABI)
+    model = tinygpt.TinyGPT({k: v.astype(np.float64) for k, v in w.items()}, cfg, batch=batch, device="cpu")
+    for name in ("x", "h", "att", "mlp", "qkv", "logits"):  # float64 buffers: exact layout check
+        setattr(model, name, getattr(model, name).double())
+    got = model.generate(prompts, steps, kv_cache=kv_cache)
+    want, _ = tinygpt64.generate(w, prompts, steps, n_layers=2, n_heads=2)
+    return got, want
+
+
+def test_driver_layout_kv_cache(monkeypatch):
+    got, want = run_host(monkeypatch, True)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_driver_layout_recompute(monkeypatch):
+    got, want = run_host(monkeypatch, False)
+    np.testing.assert_array_equal(got, want)

@@ -76,6 +76,25 @@ __device__ __forceinline__ void load_a(const GemmArgs &g, int t, int64_t m0, int
     }
 }
 
+// Interior tiles of row-major A and B (every row, column and k of the tile in bounds): the
+// same loads as load_a / load_b for VEC_ROW, unguarded, from per-thread pointers that advance
+// by one K tile per iteration.
+__device__ __forceinline__ void load_a_interior(const float *pa, int64_t s_am, float (&r)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 v = *reinterpret_cast<const float4 *>(pa + 32 * i * s_am);
+        r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
+    }
+}
+
+__device__ __forceinline__ void load_b_interior(const float *pb, int64_t s_bk, float (&r)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 v = *reinterpret_cast<const float4 *>(pb + 8 * i * s_bk);
+        r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
+    }
+}
+
 template <int A_L>
 __device__ __forceinline__ void store_a(const GemmArgs &g, int t, float (&As)[GBK][kStrideAT], const float (&r)[16]) {
     if constexpr (A_L == VEC_ROW) {
@@ -195,8 +214,20 @@ __global__ __launch_bounds__(GTHREADS) void gemm_f32_kernel(GemmArgs g) {
 
     float ra[16], rb[16];
     const int nk = (int)((g.K + GBK - 1) / GBK);
-    load_a<A_L>(g, t, m0, 0, ra);
-    load_b<B_L>(g, t, 0, n0, rb);
+    // row-major A and B on an interior tile: unguarded loads through advancing pointers for every
+    // K tile that lies wholly inside K (the last partial one takes the guarded loaders)
+    constexpr bool kRowMajor = A_L == VEC_ROW && B_L == VEC_ROW;
+    const bool interior = kRowMajor && m0 + GBM <= g.M && n0 + GBN <= g.N;
+    const int nk_full = (int)(g.K / GBK);
+    const float *pa = g.a + (m0 + (t >> 3)) * g.s_am + 4 * (t & 7);
+    const float *pb = g.b + (int64_t)(t >> 5) * g.s_bk + n0 + 4 * (t & 31);
+    if (kRowMajor && interior && nk_full > 0) {
+        load_a_interior(pa, g.s_am, ra);
+        load_b_interior(pb, g.s_bk, rb);
+    } else {
+        load_a<A_L>(g, t, m0, 0, ra);
+        load_b<B_L>(g, t, 0, n0, rb);
+    }
     store_a<A_L>(g, t, As[0], ra);
     store_b<B_L, SB>(g, t, Bs[0], rb);
     __syncthreads();
@@ -205,8 +236,15 @@ __global__ __launch_bounds__(GTHREADS) void gemm_f32_kernel(GemmArgs g) {
         const int cur = kt & 1;
         const bool more = kt + 1 < nk;
         if (more) {
-            load_a<A_L>(g, t, m0, (int64_t)(kt + 1) * GBK, ra);
-            load_b<B_L>(g, t, (int64_t)(kt + 1) * GBK, n0, rb);
+            if (kRowMajor && interior && kt + 1 < nk_full) {
+                pa += GBK;
+                pb += GBK * g.s_bk;
+                load_a_interior(pa, g.s_am, ra);
+                load_b_interior(pb, g.s_bk, rb);
+            } else {
+                load_a<A_L>(g, t, m0, (int64_t)(kt + 1) * GBK, ra);
+                load_b<B_L>(g, t, (int64_t)(kt + 1) * GBK, n0, rb);
+            }
         }
 #pragma unroll
         for (int s = 0; s < GBK / 2; s++) {

@@ -40,6 +40,19 @@ def parse():
 
 
 CAL_ELEMS = 64 * 2 ** 20  # calibration add: reads 2 x 256 MiB, writes 256 MiB
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_bench_kernels.json")
+
+
+def measured_traffic(workload):
+    """HBM bytes per launch of a benchmark workload from the committed counter summary (two
+    rocprofv3 --pmc passes, FETCH_SIZE then WRITE_SIZE, over `bench.py --pmc-probe`, scaled
+    by the calibration add), or None when the summary does not cover it."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)["kernels"][workload]
+    except (OSError, KeyError, ValueError):
+        return None
+    return int(round(t["traffic_bytes"]))
 
 
 def pmc_probe(n):
@@ -166,7 +179,7 @@ def bench_softmax(n, rows=4096, launches=48):
     del xs, ys
     torch.cuda.empty_cache()
     return dict(n=n, rows=rows, bytes=pair_bytes, us=round(avg * 1e6, 3), gbs=round(pair_bytes / avg / 1e9, 1),
-                frac=round(pair_bytes / avg / PEAK_HBM, 4))
+                frac=round(pair_bytes / avg / PEAK_HBM, 4), traffic=measured_traffic(f"softmax {rows} x {n}"))
 
 
 def bench_attention(launches=32):
@@ -187,7 +200,8 @@ def bench_attention(launches=32):
     flops = attention_flops(N, D, causal=True, heads=H)
     nbytes = 4 * 4 * H * N * D
     return dict(shape=[H, N, D], causal=True, us=round(avg * 1e6, 3), tflops=round(flops / avg / 1e12, 3),
-                frac_mfma=round(flops / avg / PEAK_FP32_MFMA, 4), gbs=round(nbytes / avg / 1e9, 1))
+                frac_mfma=round(flops / avg / PEAK_FP32_MFMA, 4), gbs=round(nbytes / avg / 1e9, 1),
+                traffic=measured_traffic(f"attention {H} x {N} x {D} causal"))
 
 
 def bench_mlp(reps=3):
@@ -224,25 +238,28 @@ def bench_tinygpt():
 
 def cpu_baseline(a, b, budget_s=10.0):
     """The oracle's matmul (round-toward-zero restatement, vectorised, all host threads up to
-    16) on the first rows of the same product; rows grow until about budget_s of work."""
+    16) over row blocks of the same product, cycling through A's rows, until about budget_s
+    of work."""
     import numpy as np
 
     import oracle
     an, bn = a.cpu().numpy(), b.cpu().numpy()
     threads = max(1, min(16, os.cpu_count() or 1))
-    n, K = bn.shape[1], bn.shape[0]
-    rows, spent, total_rows = threads, 0.0, 0
-    while spent < budget_s and total_rows + rows <= an.shape[0]:
+    M, n, K = an.shape[0], bn.shape[1], bn.shape[0]
+    rows, spent, total_rows, r0 = threads, 0.0, 0, 0
+    while spent < budget_s:
+        rows = min(rows, M - r0)
         t0 = time.perf_counter()
-        oracle.matmul_fast(an[total_rows:total_rows + rows], bn, threads=threads)
+        oracle.matmul_fast(an[r0:r0 + rows], bn, threads=threads)
         dt = time.perf_counter() - t0
         spent += dt
         total_rows += rows
+        r0 = (r0 + rows) % M
         if dt < budget_s / 8:
             rows *= 2
     flops = 2.0 * total_rows * n * K
     return dict(value=flops / spent / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"{total_rows} rows of C = A B at {an.shape[0]}x{n}x{K} ({spent:.1f} s)")
+                sample=f"{total_rows} rows of C = A B at {M}x{n}x{K}, cycling over A's rows ({spent:.1f} s)")
 
 
 def main():
@@ -282,7 +299,7 @@ def main():
                    "M": n, "N": n, "K": n, "group_size_m": 8, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 3),
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": measured_traffic(f"matmul {n}^3"),
                      "kernel_us": round(avg * 1e6, 2)},
         "device": {k: info[k] for k in ("arch", "cu_count", "max_clock_khz", "hbm_bytes")},
     }

@@ -2,7 +2,7 @@
 
     python -m piton_amd.profiling KT_DIR FETCH_DIR WRITE_DIR [--json OUT]
 
-KT_DIR holds a `--kernel-trace --stats` run of `python3 bench.py` (*_kernel_stats.csv);
+KT_DIR holds a `--kernel-trace --stats` run of `python3 bench.py` (*_kernel_trace.csv);
 FETCH_DIR / WRITE_DIR hold `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of
 `python3 bench.py --pmc-probe` (*_counter_collection.csv). Prints a markdown summary: each
 kernel's average duration, and its HBM traffic per launch, each counter scaled by the factor
@@ -22,13 +22,15 @@ import sys
 CAL_READ = 2 * 64 * 2 ** 20 * 4
 CAL_WRITE = 64 * 2 ** 20 * 4
 
-# algorithmic HBM bytes per launch of each benchmark kernel (grid size identifies the shape)
-ALGORITHMIC = {
-    "gemm_f32_kernel": ("matmul 4096^3", 3 * 4096 * 4096 * 4),
-    "softmax_rows_kernel<4": ("softmax 4096 x 1024", 2 * 4 * 4096 * 1024),
-    "softmax_rows_kernel<16": ("softmax 4096 x 4096", 2 * 4 * 4096 * 4096),
-    "softmax_rows_kernel<8": ("softmax 4096 x 1823", 2 * 4 * 4096 * 1823),
-    "attn_fwd_kernel_f32": ("attention 32 x 1024 x 64 causal", 4 * 32 * 1024 * 64 * 4),
+# benchmark launches, identified by kernel name prefix and Grid_Size_X (work-items):
+# (workload, algorithmic HBM bytes per launch, algorithmic FLOPs per launch)
+BENCH = {
+    ("gemm_f32_kernel<0, 0>", 262144): ("matmul 4096^3", 3 * 4096 * 4096 * 4, 2 * 4096 ** 3),
+    ("softmax_rows_kernel<4, 1, true>", 262144): ("softmax 4096 x 1024", 2 * 4 * 4096 * 1024, None),
+    ("softmax_rows_kernel<16, 2, true>", 131072): ("softmax 4096 x 4096", 2 * 4 * 4096 * 4096, None),
+    ("softmax_rows_kernel<8, 2, false>", 131072): ("softmax 4096 x 1823", 2 * 4 * 4096 * 1823, None),
+    ("attn_fwd_kernel_f32<64, 0>", 262144): ("attention 32 x 1024 x 64 causal", 4 * 32 * 1024 * 64 * 4,
+                                             4 * 1024 * 1024 * 64 * 32 // 2),
 }
 
 
@@ -46,11 +48,17 @@ def _one(pattern):
 
 
 def kernel_stats(kt_dir):
+    """Per (kernel, grid) launch statistics from the per-dispatch trace."""
+    groups = {}
+    for r in csv.DictReader(open(_one(os.path.join(kt_dir, "*_kernel_trace.csv")))):
+        if "piton::" in r["Kernel_Name"]:
+            key = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]))
+            groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
     rows = []
-    for r in csv.DictReader(open(_one(os.path.join(kt_dir, "*_kernel_stats.csv")))):
-        if "piton::" in r["Name"]:
-            rows.append(dict(kernel=short(r["Name"]), calls=int(r["Calls"]), avg_ns=float(r["AverageNs"]),
-                             min_ns=float(r["MinNs"]), max_ns=float(r["MaxNs"])))
+    for (k, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        d = sorted(d)
+        rows.append(dict(kernel=k, grid=grid, calls=len(d), avg_ns=sum(d) / len(d), min_ns=d[0],
+                         median_ns=d[len(d) // 2], max_ns=d[-1], workload=BENCH.get((k, grid), ("",))[0]))
     return rows
 
 
@@ -59,24 +67,25 @@ def counters(pmc_dir, counter):
     for r in csv.DictReader(open(_one(os.path.join(pmc_dir, "*_counter_collection.csv")))):
         if r["Counter_Name"] != counter or "piton::" not in r["Kernel_Name"]:
             continue
-        key = short(r["Kernel_Name"])
+        key = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
         agg.setdefault(key, []).append(float(r["Counter_Value"]) * 1024.0)  # KiB -> bytes
     return {k: sum(v) / len(v) for k, v in agg.items()}
 
 
 def summarize(kt_dir, fetch_dir, write_dir):
     fetch, write = counters(fetch_dir, "FETCH_SIZE"), counters(write_dir, "WRITE_SIZE")
-    cal = [k for k in fetch if k.startswith("add_vec4_kernel")]
+    cal = [k for k in fetch if k[0].startswith("add_vec4_kernel")]
     if not cal:
         raise RuntimeError("no calibration add in the counter runs")
     f_fetch = CAL_READ / fetch[cal[0]]
     f_write = CAL_WRITE / write[cal[0]]
     traffic = {}
     for k in fetch:
-        if k in write and not k.startswith("add_vec4"):
-            label, algo = next(((lab, b) for key, (lab, b) in ALGORITHMIC.items() if k.startswith(key)), (k, None))
-            traffic[k] = dict(workload=label, fetch_bytes=fetch[k] * f_fetch, write_bytes=write[k] * f_write,
-                              traffic_bytes=fetch[k] * f_fetch + write[k] * f_write, algorithmic_bytes=algo)
+        if k in write and k in BENCH:
+            label, algo, _ = BENCH[k]
+            traffic[label] = dict(kernel=k[0], grid=k[1], fetch_bytes=fetch[k] * f_fetch,
+                                  write_bytes=write[k] * f_write,
+                                  traffic_bytes=fetch[k] * f_fetch + write[k] * f_write, algorithmic_bytes=algo)
     return kernel_stats(kt_dir), traffic, f_fetch, f_write
 
 
@@ -89,21 +98,26 @@ def main(argv=None):
     a = ap.parse_args(argv)
     stats, traffic, ff, fw = summarize(a.kt_dir, a.fetch_dir, a.write_dir)
     out = sys.stdout
-    out.write("## Kernel durations (rocprofv3 --kernel-trace --stats)\n\n")
-    out.write("| kernel | calls | avg us | min us | max us |\n|---|---|---|---|---|\n")
+    out.write("## Kernel durations (rocprofv3 --kernel-trace, per dispatch, grouped by grid)\n\n")
+    out.write("| kernel | grid (work-items) | benchmark workload | calls | avg us | median us | min us | max us | "
+              "achieved |\n|---|---|---|---|---|---|---|---|---|\n")
     for r in stats:
-        out.write(f"| `{r['kernel']}` | {r['calls']} | {r['avg_ns'] / 1e3:.2f} | {r['min_ns'] / 1e3:.2f} | "
-                  f"{r['max_ns'] / 1e3:.2f} |\n")
+        bench = BENCH.get((r["kernel"], r["grid"]))
+        ach = ""
+        if bench:
+            _, nbytes, flops = bench
+            ach = (f"{flops / r['avg_ns'] / 1e3:.1f} TFLOP/s" if flops else f"{nbytes / r['avg_ns']:.0f} GB/s")
+        out.write(f"| `{r['kernel']}` | {r['grid']} | {r['workload']} | {r['calls']} | {r['avg_ns'] / 1e3:.2f} | "
+                  f"{r['median_ns'] / 1e3:.2f} | {r['min_ns'] / 1e3:.2f} | {r['max_ns'] / 1e3:.2f} | {ach} |\n")
     out.write(f"\n## HBM traffic per launch (FETCH_SIZE x {ff:.3f}, WRITE_SIZE x {fw:.3f})\n\n")
     out.write("Scale factors: the calibration add reads 512 MiB and writes 256 MiB; the counters read "
               f"{CAL_READ / ff / 2 ** 20:.1f} MiB and {CAL_WRITE / fw / 2 ** 20:.1f} MiB for it.\n\n")
-    out.write("| kernel | workload | fetch MB | write MB | traffic MB | algorithmic MB | traffic / algorithmic |\n")
+    out.write("| workload | kernel | fetch MB | write MB | traffic MB | algorithmic MB | traffic / algorithmic |\n")
     out.write("|---|---|---|---|---|---|---|\n")
-    for k, t in traffic.items():
+    for label, t in traffic.items():
         algo = t["algorithmic_bytes"]
-        ratio = f"{t['traffic_bytes'] / algo:.2f}" if algo else "-"
-        out.write(f"| `{k}` | {t['workload']} | {t['fetch_bytes'] / 1e6:.1f} | {t['write_bytes'] / 1e6:.1f} | "
-                  f"{t['traffic_bytes'] / 1e6:.1f} | {algo / 1e6 if algo else float('nan'):.1f} | {ratio} |\n")
+        out.write(f"| {label} | `{t['kernel']}` | {t['fetch_bytes'] / 1e6:.1f} | {t['write_bytes'] / 1e6:.1f} | "
+                  f"{t['traffic_bytes'] / 1e6:.1f} | {algo / 1e6:.1f} | {t['traffic_bytes'] / algo:.2f} |\n")
     if a.json:
         with open(a.json, "w") as f:
             json.dump(dict(fetch_factor=ff, write_factor=fw, kernels=traffic), f, indent=1)

@@ -10,7 +10,7 @@
  *     and piton_mi355x_last_error() gives this thread's message for the last failure.
  *
  * Each kernel entry replaces one `kernel[grid](...)` launch of the reference
- * (piton/runtime/launcher.py:270-292, the `device == "emu"` / `"pi"` dispatch at :285-291),
+ * (piton/runtime/launcher.py:217-245, the `device == "emu"` / `"pi"` dispatch at :238-244),
  * with the reference kernel's runtime arguments in the same order and meaning.
  */
 #ifndef PITON_MI355X_H

@@ -1,5 +1,5 @@
 """`kernel[grid](*args, device="mi355x")` for PIton kernels (piton/runtime/launcher.py:42-63,
-264-292), dispatched to libpiton_mi355x.so.
+217-245), dispatched to libpiton_mi355x.so.
 
 Arguments follow the reference's conventions: `bind` splits them into signature, constants and
 runtime values exactly as PIton does (constexpr-annotated parameters and ints equal to 1 become
@@ -8,7 +8,7 @@ constants), so a kernel's arguments are read from `dict(values, **constants)`. A
     asynchronous on torch's current stream, as a GPU Triton launch is;
   * numpy float32 / int32 / uint32 arrays: every array is copied to the device, the kernel
     runs, and every array is copied back, inputs included, before the call returns (the
-    emulator's copy-in / copy-out contract, launcher.py:223-258).
+    emulator's copy-in / copy-out contract, launcher.py:175-180, 209-211).
 
 The kernel is identified by its name and parameter list; the grid must be the kernel's
 canonical cover for the given constexprs (any other grid would compute a different set of
@@ -36,7 +36,7 @@ def _is_tensor(v) -> bool:
 
 
 def _sig_of(value):
-    """The signature type of a runtime argument (piton/runtime/launcher.py:75-86), plus
+    """The signature type of a runtime argument (piton/runtime/launcher.py:28-39), plus
     torch tensors."""
     if isinstance(value, np.ndarray):
         if value.dtype not in _DTYPE_SIG:
@@ -59,7 +59,7 @@ def _sig_of(value):
 
 def bind(fn, args, kwargs, do_not_specialize=()):
     """Split launch arguments into (signature, constants, runtime values), as
-    piton/runtime/launcher.py:89-110 does."""
+    piton/runtime/launcher.py:42-63 does."""
     params = list(inspect.signature(fn).parameters.values())
     bound = inspect.signature(fn).bind_partial(*args, **kwargs)
     signature, constants, values = {}, {}, {}
@@ -84,7 +84,7 @@ def bind(fn, args, kwargs, do_not_specialize=()):
 
 @dataclass
 class LaunchRecord:
-    """What a launch returns (the reference returns its CompiledKernel, launcher.py:292)."""
+    """What a launch returns (the reference returns its CompiledKernel, launcher.py:245)."""
     name: str
     grid: tuple
     entry: str

@@ -1,6 +1,6 @@
 """The drop-in boundary on any host: the C ABI library loads and exports every entry its
 header declares, rejects bad arguments before touching a device, reports a missing device;
-the launch surface binds arguments as PIton does (piton/runtime/launcher.py:89-110) and
+the launch surface binds arguments as PIton does (piton/runtime/launcher.py:42-63) and
 checks grids before anything reaches the device."""
 import ctypes
 import glob

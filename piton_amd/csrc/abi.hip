@@ -20,6 +20,10 @@ int set_error(int code, const char *fmt, ...) {
 
 void clear_error() { g_msg[0] = '\0'; }
 
+static thread_local int g_cu_count = 0;
+
+int device_cu_count() { return g_cu_count; }
+
 int require_device() {
     // the architecture check is cached per thread and device: later calls cost one
     // hipGetDevice
@@ -38,6 +42,7 @@ int require_device() {
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return set_error(PITON_ENODEV, "device %d is %s; this library is built for gfx950", dev, p.gcnArchName);
     checked_dev = dev;
+    g_cu_count = p.multiProcessorCount;
     return PITON_OK;
 }
 

@@ -20,6 +20,8 @@ int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3
 void clear_error();
 // PITON_OK when a gfx950 device is current, else PITON_ENODEV / PITON_EHIP with a message.
 int require_device();
+// Compute units of the device the last successful require_device() on this thread checked.
+int device_cu_count();
 // Turns the last launch's status into PITON_OK or PITON_EHIP naming `what`.
 int check_launch(const char *what);
 

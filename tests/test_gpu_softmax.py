@@ -95,11 +95,18 @@ def test_row_strides_and_alignments(in_stride, out_stride, n):
     assert (got[:, n:] == -5.0).all()
 
 
-def test_long_rows_take_the_multipass_kernel():
-    rng = np.random.default_rng(2)
-    x = (rng.standard_normal((5, 10000)) * 3).astype(np.float32)
+@pytest.mark.parametrize("n", [2048, 2047, 4093, 6000, 6001, 10000, 10001, 16384, 16385, 20000])
+def test_row_lengths_of_every_kernel(n):
+    """Lengths that take each workgroup-per-row variant (2, 4, 8, 16 chunks per thread;
+    aligned and not) and the three-pass kernel for rows past 16K columns; one row holds a
+    +inf, one a -inf."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((5, n)) * 3).astype(np.float32)
+    x[1, n // 2] = np.inf
+    x[2, 0] = -np.inf
     got = run(torch.from_numpy(x).cuda()).cpu().numpy()
-    check(got, x, 10000)
+    check(got, x, n)
+    assert np.isnan(got[1]).all() and got[2, 0] == 0.0
 
 
 def test_in_place():

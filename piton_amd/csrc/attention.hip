@@ -26,6 +26,8 @@
 //     loads (consecutive keys across lanes) for pre-transposed [D, N] storage.
 #include "common.h"
 
+#include <algorithm>
+
 namespace piton {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -77,26 +79,13 @@ __device__ __forceinline__ void load_k_operand(const AttnArgs &g, const float *k
     }
 }
 
-// A wave computes a 32-query group against key blocks w, w + ANW, ... straight from global
-// memory (no LDS, no barrier):
-//   S^T = K Q'^T   A: K half rows (contiguous), B: Q' half rows held for the whole kernel;
-//   online softmax in the lane (lane % 32 is the query) plus one exchange with lane ^ 32;
-//   O^T += V^T P^T A: V rows, 32 consecutive dims per half wave (128-byte coalesced), B: the
-//   lane's own score registers (key order permuted to the MFMA output layout).
-// The ANW partial states of the group merge through LDS at the end.
-template <int D, int KL>
-__global__ __launch_bounds__(64 * ANW) __attribute__((amdgpu_waves_per_eu(D <= 64 ? PITON_ATTN_WAVES_PER_EU : 1)))
-void attn_fwd_kernel_f32(AttnArgs g) {
-    __shared__ float vslab[ANW][ABN][D];  // per-wave V staging; reused for the merge
-    float(*xo)[D / 2][64] = reinterpret_cast<float(*)[D / 2][64]>(&vslab[0][0][0]);
-    float(*xm)[2][64] = reinterpret_cast<float(*)[2][64]>(&vslab[0][0][0] + (ANW - 1) * (D / 2) * 64);
+// ---- the per-block steps both forward kernels share (identical arithmetic) ----------------
 
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, half = lane >> 5, l31 = lane & 31;
-    // workgroup -> (head, query group): the dispatcher deals workgroups round-robin over the
-    // XCDs, so give each XCD whole heads (their K and V stay in that XCD's L2), and within an
-    // XCD issue the longest causal groups of all its heads first
+// workgroup -> (batch*head, query group): the dispatcher deals workgroups round-robin over the
+// XCDs, so give each XCD whole heads (their K and V stay in that XCD's L2), and within an XCD
+// issue the longest causal groups of all its heads first
+__device__ __forceinline__ void map_group(const AttnArgs &g, int64_t &bh, int &qg) {
     const int nqg = g.nqg, nbh = g.nbh;
-    int64_t bh;
     int qrank;
     if (nbh % kXcdCount == 0) {
         const int xcd = blockIdx.x % kXcdCount, i = blockIdx.x / kXcdCount, per = nbh / kXcdCount;
@@ -106,7 +95,139 @@ void attn_fwd_kernel_f32(AttnArgs g) {
         bh = blockIdx.x / nqg;
         qrank = blockIdx.x % nqg;
     }
-    const int qg = g.causal ? nqg - 1 - qrank : qrank;
+    qg = g.causal ? nqg - 1 - qrank : qrank;
+}
+
+// S^T = K Q'^T for one block of 32 keys: lane (half, l31) gets 16 scores of query l31, register r
+// holding key 8*(r/4) + 4*half + r%4 of the block
+template <int D>
+__device__ __forceinline__ f32x16 block_scores(const float (&kf)[D / 2], const float (&qf)[D / 2]) {
+    f32x16 st;
+#pragma unroll
+    for (int r = 0; r < 16; r++) st[r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < D / 2; s++) st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[s], st, 0, 0, 0);
+    return st;
+}
+
+// keys past n_ctx, and under causal masking keys after the query, score -inf; only blocks that
+// can hold such a key pay for the test
+__device__ __forceinline__ void mask_scores(f32x16 &st, int key0, int n_ctx, int causal, int q0, int qi, int half) {
+    if (key0 + ABN > n_ctx || (causal && key0 + ABN - 1 > q0)) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int key = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (key >= n_ctx || (causal && key > qi)) st[r] = -INFINITY;
+        }
+    }
+}
+
+// Online softmax with a lazily moved reference: each query keeps a reference maximum m_i (log2
+// units) and moves it only when a block's scores exceed it by more than kSlack. Then
+// p = 2^(s - m_i) <= 2^kSlack (no overflow: l stays below 2^kSlack times the key count), and O
+// and l are rescaled only on the rare blocks that move some query's reference, instead of on
+// every block. The quotient O / l is the same mathematically; rounding differs by a few ulp.
+// Turns st into p in place.
+constexpr float kSlack = 8.f;
+
+template <int D>
+__device__ __forceinline__ void online_update(f32x16 &st, float &m_i, float &l_i, f32x16 (&o)[D / 32]) {
+    float mloc = st[0];
+#pragma unroll
+    for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, st[r]);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));  // the other half of the wave holds the query's other keys
+    const bool move = mloc > m_i + kSlack;     // m_i = -inf: moves on the first visible score
+    if (__any(move)) {
+        const float m_new = move ? mloc : m_i;
+        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);  // 0 from -inf, 1 if not moved
+#pragma unroll
+        for (int b = 0; b < D / 32; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[b][r] *= alpha;
+        l_i *= alpha;
+        m_i = m_new;
+    }
+    const float mref = m_i == -INFINITY ? 0.f : m_i;  // nothing visible yet: every p is 0
+    float lsum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        st[r] = __builtin_amdgcn_exp2f(st[r] - mref);
+        lsum += st[r];
+    }
+    l_i += lsum + __shfl_xor(lsum, 32);
+}
+
+// O^T += V^T P^T from the wave's V slab (vw[key][dim]): step s pairs key (s/4)*8 + 4*half + s%4
+// with dim b*32 + l31, and its B operand is the lane's own p register s
+template <int D>
+__device__ __forceinline__ void block_pv(f32x16 (&o)[D / 32], const f32x16 &p, const float (*vw)[D], int half, int l31) {
+#pragma unroll
+    for (int b = 0; b < D / 32; b++)
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const float a = vw[(s >> 2) * 8 + 4 * half + (s & 3)][b * 32 + l31];
+            o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, p[s], o[b], 0, 0, 0);
+        }
+}
+
+// Merges the ANW partial states of the group: waves 1.. hand (m, l, O) over LDS (same lane =
+// same query and output element), wave 0 combines and stores row qi of the output.
+template <int D>
+__device__ __forceinline__ void merge_store(float *lds, const f32x16 (&o)[D / 32], float m_i, float l_i, float *op,
+                                            bool row_ok, int head_dim) {
+    float(*xo)[D / 2][64] = reinterpret_cast<float(*)[D / 2][64]>(lds);
+    float(*xm)[2][64] = reinterpret_cast<float(*)[2][64]>(lds + (ANW - 1) * (D / 2) * 64);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5;
+    __syncthreads();  // every wave is done with its V slab
+    if (wave > 0) {
+#pragma unroll
+        for (int b = 0; b < D / 32; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) xo[wave - 1][b * 16 + r][lane] = o[b][r];
+        xm[wave - 1][0][lane] = m_i;
+        xm[wave - 1][1][lane] = l_i;
+    }
+    __syncthreads();
+    if (wave == 0 && row_ok) {
+        float m = m_i;
+#pragma unroll
+        for (int w = 0; w < ANW - 1; w++) m = fmaxf(m, xm[w][0][lane]);
+        const float mu = m == -INFINITY ? 0.f : m;
+        const float c0 = __builtin_amdgcn_exp2f(m_i - mu);
+        float cw[ANW - 1];
+        float l = l_i * c0;
+#pragma unroll
+        for (int w = 0; w < ANW - 1; w++) {
+            cw[w] = __builtin_amdgcn_exp2f(xm[w][0][lane] - mu);
+            l += xm[w][1][lane] * cw[w];
+        }
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int b = 0; b < D / 32; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int d = b * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                float acc = o[b][r] * c0;
+#pragma unroll
+                for (int w = 0; w < ANW - 1; w++) acc += xo[w][b * 16 + r][lane] * cw[w];
+                if (d < head_dim) op[d] = acc * inv;
+            }
+    }
+}
+
+// The general kernel: any head_dim <= D, any strides (K also pre-transposed), guarded loads.
+// A wave computes a 32-query group against key blocks w, w + ANW, ...:
+//   S^T = K Q'^T   A: K half rows, B: Q' half rows held for the whole kernel;
+//   online softmax in the lane (lane % 32 is the query) plus one exchange with lane ^ 32;
+//   O^T += V^T P^T A: V from the wave's LDS slab, B: the lane's own p registers.
+template <int D, int KL>
+__global__ __launch_bounds__(64 * ANW) __attribute__((amdgpu_waves_per_eu(D <= 64 ? PITON_ATTN_WAVES_PER_EU : 1)))
+void attn_fwd_kernel_f32(AttnArgs g) {
+    __shared__ float vslab[ANW][ABN][D];  // per-wave V staging; reused for the merge
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, half = lane >> 5, l31 = lane & 31;
+    int64_t bh;
+    int qg;
+    map_group(g, bh, qg);
     const int64_t bi = bh / g.n_heads, h = bh % g.n_heads;
     const int64_t q0 = (int64_t)qg * AQG;
     const int64_t qi = q0 + l31;  // this lane's query
@@ -146,13 +267,9 @@ void attn_fwd_kernel_f32(AttnArgs g) {
     const int nkb_all = (n_ctx + ABN - 1) / ABN;
     const int nkb = g.causal ? min(nkb_all, qg + 1) : nkb_all;
 
-    // V of block kb goes through this wave's own LDS slab: float4 rows in, V^T operand columns
-    // out (one wave writes and reads it, in order: no barrier); V rows are loaded at the top of
-    // their block, K half rows one block ahead
     float(*vw)[D] = reinterpret_cast<float(*)[D]>(&vslab[wave][0][0]);
     constexpr int NVQ = ABN * D / 4 / 64;  // float4 chunks of a V block per lane
-    auto load_v = [&](int kb, float4 (&vr)[NVQ]) {
-        const int key0 = kb * ABN;
+    auto load_v = [&](int key0, float4 (&vr)[NVQ]) {
         const bool full = key0 + ABN <= n_ctx && D == g.head_dim && g.v_vec;
 #pragma unroll
         for (int c = 0; c < NVQ; c++) {
@@ -170,113 +287,156 @@ void attn_fwd_kernel_f32(AttnArgs g) {
             }
         }
     };
-    auto process = [&](int kb, const float (&kf)[D / 2]) {
-        const int key0 = kb * ABN;
-        float4 vr[NVQ];
-        load_v(kb, vr);  // in flight during the score product
-        f32x16 st;
-#pragma unroll
-        for (int r = 0; r < 16; r++) st[r] = 0.f;
-#pragma unroll
-        for (int s = 0; s < D / 2; s++) st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[s], st, 0, 0, 0);
-
-        // masks, only on blocks that can hold a masked key: register r holds key
-        // key0 + 8*(r/4) + 4*half + r%4 of query qi
-        if (key0 + ABN > n_ctx || (g.causal && key0 + ABN - 1 > (int)q0)) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (key >= n_ctx || (g.causal && key > qi32)) st[r] = -INFINITY;
-            }
-        }
-        float mloc = st[0];
-#pragma unroll
-        for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, st[r]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float m_new = fmaxf(m_i, mloc);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;  // rows with nothing visible yet
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
-        float lsum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            st[r] = __builtin_amdgcn_exp2f(st[r] - m_use);
-            lsum += st[r];
-        }
-        lsum += __shfl_xor(lsum, 32);
-        l_i = l_i * alpha + lsum;
-        m_i = m_new;
-
+    auto stage_v = [&](const float4 (&vr)[NVQ]) {
 #pragma unroll
         for (int c = 0; c < NVQ; c++) {
             const int idx = lane + 64 * c;
-            *reinterpret_cast<float4 *>(&vw[idx / (D / 4)][4 * (idx % (D / 4))]) = vr[c];
-        }
-#pragma unroll
-        for (int b = 0; b < D / 32; b++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) o[b][r] *= alpha;
-#pragma unroll
-            for (int s = 0; s < 16; s++) {
-                // V^T operand: step s pairs key (s/4)*8 + 4*half + s%4 with dim b*32 + l31
-                const float a = vw[(s >> 2) * 8 + 4 * half + (s & 3)][b * 32 + l31];
-                o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, st[s], o[b], 0, 0, 0);
-            }
+            *reinterpret_cast<f32x4 *>(&vw[idx / (D / 4)][4 * (idx % (D / 4))]) =
+                f32x4{vr[c].x, vr[c].y, vr[c].z, vr[c].w};
         }
     };
+    auto process = [&](int kb, const float (&kf)[D / 2]) {
+        const int key0 = kb * ABN;
+        float4 vr[NVQ];
+        if constexpr (D <= 64) load_v(key0, vr);  // in flight during the score product
+        f32x16 st = block_scores<D>(kf, qf);
+        if constexpr (D > 64) load_v(key0, vr);  // after it: Q, K, O and S already fill the registers
+        mask_scores(st, key0, n_ctx, g.causal, (int)q0, qi32, half);
+        online_update<D>(st, m_i, l_i, o);
+        wave_lds_sync();  // the previous block's operand reads are done with the slab
+        stage_v(vr);
+        wave_lds_sync();  // rows staged by other lanes are visible to the operand reads
+        block_pv<D>(o, st, vw, half, l31);
+    };
 
-    // two K stages, unrolled by two so neither is copied: block kb + ANW's K loads while kb is
-    // multiplied
+    int kb = wave;
+    if constexpr (D <= 64) {
+        // two K stages, unrolled by two so neither is copied: block kb + ANW's K loads while kb
+        // is multiplied
+        float kf0[D / 2], kf1[D / 2];
+        if (kb < nkb) load_k_operand<D, KL>(g, kbase, kb * ABN + l31, half, kf0);
+        while (kb < nkb) {
+            if (kb + ANW < nkb) load_k_operand<D, KL>(g, kbase, (kb + ANW) * ABN + l31, half, kf1);
+            process(kb, kf0);
+            kb += ANW;
+            if (kb >= nkb) break;
+            if (kb + ANW < nkb) load_k_operand<D, KL>(g, kbase, (kb + ANW) * ABN + l31, half, kf0);
+            process(kb, kf1);
+            kb += ANW;
+        }
+    } else {
+        // D = 128: one K stage, loaded at the top of its block, so that no phase holds more than
+        // 256 values per lane
+        for (; kb < nkb; kb += ANW) {
+            float kf[D / 2];
+            load_k_operand<D, KL>(g, kbase, kb * ABN + l31, half, kf);
+            process(kb, kf);
+        }
+    }
+    merge_store<D>(&vslab[0][0][0], o, m_i, l_i, g.o + bi * g.s_ob + h * g.s_oh + qi * g.s_om, qi < g.n_ctx,
+                   g.head_dim);
+}
+
+// Raw buffer descriptor over [base, base + bytes): loads at byte offsets >= bytes return 0, so
+// blocks past the end of the sequence need no guards.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// The fast kernel: head_dim == D, Q / K / V rows contiguous and 16-byte aligned (K in [N, D]
+// order), every row offset of a head within 2^31 bytes (checked on the host). Same blocks and
+// arithmetic as the general kernel, but Q, K and V come through buffer descriptors bounded at
+// the head's last row: a lane's addresses are 32-bit byte offsets that advance by one constant
+// per block, rows past n_ctx read as zeros, and nothing is guarded.
+template <int D>
+__global__ __launch_bounds__(64 * ANW) __attribute__((amdgpu_waves_per_eu(PITON_ATTN_WAVES_PER_EU)))
+void attn_fwd_fast(AttnArgs g) {
+    __shared__ float vslab[ANW][ABN][D];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, half = lane >> 5, l31 = lane & 31;
+    int64_t bh;
+    int qg;
+    map_group(g, bh, qg);
+    const int64_t bi = bh / g.n_heads, h = bh % g.n_heads;
+    const int q0 = qg * AQG, qi = q0 + l31, n_ctx = (int)g.n_ctx;
+    const uint32_t s_qm = (uint32_t)g.s_qm, s_kn = (uint32_t)g.s_kn, s_vn = (uint32_t)g.s_vn;
+
+    const auto rq = make_rsrc(g.q + bi * g.s_qb + h * g.s_qh, ((uint32_t)(n_ctx - 1) * s_qm + D) * 4u);
+    const auto rk = make_rsrc(g.k + bi * g.s_kb + h * g.s_kh, ((uint32_t)(n_ctx - 1) * s_kn + D) * 4u);
+    const auto rv = make_rsrc(g.v + bi * g.s_vb + h * g.s_vh, ((uint32_t)(n_ctx - 1) * s_vn + D) * 4u);
+
+    float qf[D / 2];
+    {
+        const uint32_t off = ((uint32_t)qi * s_qm + half * (D / 2)) * 4u;
+#pragma unroll
+        for (int c = 0; c < D / 8; c++) {
+            const f32x4 f = bload4(rq, off + 16u * c);
+#pragma unroll
+            for (int j = 0; j < 4; j++) qf[4 * c + j] = f[j] * g.scale;
+        }
+    }
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int b = 0; b < D / 32; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[b][r] = 0.f;
+    float m_i = -INFINITY, l_i = 0.f;
+
+    const int nkb_all = (n_ctx + ABN - 1) / ABN;
+    const int nkb = g.causal ? min(nkb_all, qg + 1) : nkb_all;
+
+    // byte offsets: K half row of key kb*32 + l31; V chunk c of the block at v_off + c * v_c
+    constexpr int KPC = 64 / (D / 4);  // V keys per float4 chunk step of the lane
+    constexpr int NVQ = ABN * D / 4 / 64;
+    uint32_t k_off = ((uint32_t)(wave * ABN + l31) * s_kn + half * (D / 2)) * 4u;
+    uint32_t v_off = ((uint32_t)(wave * ABN + lane / (D / 4)) * s_vn + 4 * (lane % (D / 4))) * 4u;
+    const uint32_t k_step = (uint32_t)(ANW * ABN) * s_kn * 4u, v_step = (uint32_t)(ANW * ABN) * s_vn * 4u;
+    const uint32_t v_c = (uint32_t)KPC * s_vn * 4u;
+
+    float(*vw)[D] = reinterpret_cast<float(*)[D]>(&vslab[wave][0][0]);
+    auto load_k = [&](float (&kf)[D / 2]) {
+#pragma unroll
+        for (int c = 0; c < D / 8; c++) {
+            const f32x4 f = bload4(rk, k_off + 16u * c);
+#pragma unroll
+            for (int j = 0; j < 4; j++) kf[4 * c + j] = f[j];
+        }
+        k_off += k_step;
+    };
+    auto process = [&](int kb, const float (&kf)[D / 2]) {
+        f32x4 vr[NVQ];
+#pragma unroll
+        for (int c = 0; c < NVQ; c++) vr[c] = bload4(rv, v_off + v_c * c);
+        v_off += v_step;
+        f32x16 st = block_scores<D>(kf, qf);
+        mask_scores(st, kb * ABN, n_ctx, g.causal, q0, qi, half);
+        online_update<D>(st, m_i, l_i, o);
+        wave_lds_sync();  // the previous block's operand reads are done with the slab
+#pragma unroll
+        for (int c = 0; c < NVQ; c++) {
+            const int idx = lane + 64 * c;
+            *reinterpret_cast<f32x4 *>(&vw[idx / (D / 4)][4 * (idx % (D / 4))]) = vr[c];
+        }
+        wave_lds_sync();  // rows staged by other lanes are visible to the operand reads
+        block_pv<D>(o, st, vw, half, l31);
+    };
+
     float kf0[D / 2], kf1[D / 2];
     int kb = wave;
-    if (kb < nkb) load_k_operand<D, KL>(g, kbase, kb * ABN + l31, half, kf0);
+    if (kb < nkb) load_k(kf0);
     while (kb < nkb) {
-        if (kb + ANW < nkb) load_k_operand<D, KL>(g, kbase, (kb + ANW) * ABN + l31, half, kf1);
+        if (kb + ANW < nkb) load_k(kf1);
         process(kb, kf0);
         kb += ANW;
         if (kb >= nkb) break;
-        if (kb + ANW < nkb) load_k_operand<D, KL>(g, kbase, (kb + ANW) * ABN + l31, half, kf0);
+        if (kb + ANW < nkb) load_k(kf0);
         process(kb, kf1);
         kb += ANW;
     }
-
-    // merge the group's ANW partial states: waves 1.. hand (m, l, O) over LDS (same lane = same
-    // query and output element), wave 0 combines and stores; the V slabs are dead by now
-    __syncthreads();
-    if (wave > 0) {
-#pragma unroll
-        for (int b = 0; b < D / 32; b++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) xo[wave - 1][b * 16 + r][lane] = o[b][r];
-        xm[wave - 1][0][lane] = m_i;
-        xm[wave - 1][1][lane] = l_i;
-    }
-    __syncthreads();
-    if (wave == 0 && qi < g.n_ctx) {
-        float m = m_i;
-#pragma unroll
-        for (int w = 0; w < ANW - 1; w++) m = fmaxf(m, xm[w][0][lane]);
-        const float mu = m == -INFINITY ? 0.f : m;
-        const float c0 = __builtin_amdgcn_exp2f(m_i - mu);
-        float cw[ANW - 1];
-        float l = l_i * c0;
-#pragma unroll
-        for (int w = 0; w < ANW - 1; w++) {
-            cw[w] = __builtin_amdgcn_exp2f(xm[w][0][lane] - mu);
-            l += xm[w][1][lane] * cw[w];
-        }
-        const float inv = 1.0f / l;
-        float *op = g.o + bi * g.s_ob + h * g.s_oh + qi * g.s_om;
-#pragma unroll
-        for (int b = 0; b < D / 32; b++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int d = b * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                float acc = o[b][r] * c0;
-#pragma unroll
-                for (int w = 0; w < ANW - 1; w++) acc += xo[w][b * 16 + r][lane] * cw[w];
-                if (d < g.head_dim) op[d] = acc * inv;
-            }
-    }
+    merge_store<D>(&vslab[0][0][0], o, m_i, l_i, g.o + bi * g.s_ob + h * g.s_oh + (int64_t)qi * g.s_om, qi < n_ctx,
+                   D);
 }
 
 template <int D>
@@ -349,7 +509,15 @@ static int attn_launch(AttnArgs g, int64_t batch, int64_t n_heads, int32_t head_
     g.nqg = (int)((g.n_ctx + AQG - 1) / AQG);
     g.nbh = (int)(batch * n_heads);
     const dim3 grid((unsigned)((int64_t)g.nqg * g.nbh));
-    if (head_dim <= 32) launch_d<32>(kl, g, grid, st);
+    // the fast kernel: exact head_dim, contiguous aligned rows that do not overlap, and every
+    // byte offset of a head (rows up to n_ctx + 32) within 31 bits
+    const int64_t smax = std::max(g.s_qm, std::max(g.s_kn, g.s_vn));
+    const bool fast = (head_dim == 32 || head_dim == 64) && kl == K_VEC_D && g.q_vec && g.v_vec &&
+                      g.s_qm >= head_dim && g.s_kn >= head_dim && g.s_vn >= head_dim &&
+                      ((g.n_ctx + 2 * AQG) * smax + head_dim) * 4 < (1LL << 31);
+    if (fast && head_dim == 64) hipLaunchKernelGGL(attn_fwd_fast<64>, grid, dim3(64 * ANW), 0, st, g);
+    else if (fast) hipLaunchKernelGGL(attn_fwd_fast<32>, grid, dim3(64 * ANW), 0, st, g);
+    else if (head_dim <= 32) launch_d<32>(kl, g, grid, st);
     else if (head_dim == 64) launch_d<64>(kl, g, grid, st);
     else launch_d<128>(kl, g, grid, st);
     return check_launch("attn_fwd");

@@ -71,6 +71,16 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
     return op(op(a, b), op(c, d));
 }
 
+// Orders LDS traffic between the lanes of one wavefront: stores before the fence are visible
+// to loads after it in every lane of the wave. The hardware already runs a wave's LDS
+// operations in order; the fences stop the compiler from moving a load above a store that
+// another lane made (per thread the addresses differ, so it would otherwise be free to).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Workgroup order for an XCD-partitioned chip: the dispatcher hands workgroup b to XCD
 // b % n_xcd, so renumber to give each XCD a contiguous run of logical ids (neighbouring tiles
 // then share that XCD's L2). A bijection on [0, n) for any n.

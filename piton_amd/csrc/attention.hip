@@ -27,6 +27,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace piton {
 
@@ -131,7 +132,7 @@ __device__ __forceinline__ void mask_scores(f32x16 &st, int key0, int n_ctx, int
 constexpr float kSlack = 8.f;
 
 template <int D>
-__device__ __forceinline__ void online_update(f32x16 &st, float &m_i, float &l_i, f32x16 (&o)[D / 32]) {
+__device__ __forceinline__ float online_rescale(const f32x16 &st, float &m_i, float &l_i, f32x16 (&o)[D / 32]) {
     float mloc = st[0];
 #pragma unroll
     for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, st[r]);
@@ -147,7 +148,11 @@ __device__ __forceinline__ void online_update(f32x16 &st, float &m_i, float &l_i
         l_i *= alpha;
         m_i = m_new;
     }
-    const float mref = m_i == -INFINITY ? 0.f : m_i;  // nothing visible yet: every p is 0
+    return m_i == -INFINITY ? 0.f : m_i;  // nothing visible yet: every p is 0
+}
+
+// p = 2^(s - mref) in place; their sum over the query's 32 keys joins l
+__device__ __forceinline__ void online_exp(f32x16 &st, float mref, float &l_i) {
     float lsum = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
@@ -155,6 +160,11 @@ __device__ __forceinline__ void online_update(f32x16 &st, float &m_i, float &l_i
         lsum += st[r];
     }
     l_i += lsum + __shfl_xor(lsum, 32);
+}
+
+template <int D>
+__device__ __forceinline__ void online_update(f32x16 &st, float &m_i, float &l_i, f32x16 (&o)[D / 32]) {
+    online_exp(st, online_rescale<D>(st, m_i, l_i, o), l_i);
 }
 
 // O^T += V^T P^T from the wave's V slab (vw[key][dim]): step s pairs key (s/4)*8 + 4*half + s%4
@@ -405,35 +415,49 @@ void attn_fwd_fast(AttnArgs g) {
         }
         k_off += k_step;
     };
-    auto process = [&](int kb, const float (&kf)[D / 2]) {
-        f32x4 vr[NVQ];
+    auto load_v = [&](f32x4 (&vr)[NVQ]) {
 #pragma unroll
         for (int c = 0; c < NVQ; c++) vr[c] = bload4(rv, v_off + v_c * c);
         v_off += v_step;
-        f32x16 st = block_scores<D>(kf, qf);
-        mask_scores(st, kb * ABN, n_ctx, g.causal, q0, qi, half);
-        online_update<D>(st, m_i, l_i, o);
-        wave_lds_sync();  // the previous block's operand reads are done with the slab
-#pragma unroll
-        for (int c = 0; c < NVQ; c++) {
-            const int idx = lane + 64 * c;
-            *reinterpret_cast<f32x4 *>(&vw[idx / (D / 4)][4 * (idx % (D / 4))]) = vr[c];
-        }
-        wave_lds_sync();  // rows staged by other lanes are visible to the operand reads
-        block_pv<D>(o, st, vw, half, l31);
     };
 
-    float kf0[D / 2], kf1[D / 2];
+    // Software pipeline over this wave's blocks kb = wave, wave + ANW, ...: while block kb's
+    // exps run on the vector unit, block kb + ANW's score product runs on the matrix cores;
+    // each load is issued as soon as its registers are free (K right after the product that
+    // reads it, V right after it is staged), a whole block ahead of its use. Loads of a block
+    // past the last one read zeros or unused rows (never out of the buffers) and are dropped.
     int kb = wave;
-    if (kb < nkb) load_k(kf0);
-    while (kb < nkb) {
-        if (kb + ANW < nkb) load_k(kf1);
-        process(kb, kf0);
-        kb += ANW;
-        if (kb >= nkb) break;
-        if (kb + ANW < nkb) load_k(kf0);
-        process(kb, kf1);
-        kb += ANW;
+    if (kb < nkb) {
+        float kf[D / 2];
+        f32x4 vr[NVQ];
+        load_k(kf);
+        f32x16 st = block_scores<D>(kf, qf);
+        // the loop starts with the next block's K issued before this block's V, the order it
+        // keeps every iteration, so each wait on K lets the newer V loads stay in flight
+        load_k(kf);
+        __builtin_amdgcn_sched_barrier(0);  // keep that order through instruction scheduling
+        load_v(vr);
+        auto step = [&](auto has_next) {
+            constexpr bool NEXT = decltype(has_next)::value;
+            mask_scores(st, kb * ABN, n_ctx, g.causal, q0, qi, half);
+            const float mref = online_rescale<D>(st, m_i, l_i, o);
+            f32x16 st_next;
+            if constexpr (NEXT) st_next = block_scores<D>(kf, qf);
+            online_exp(st, mref, l_i);
+            if constexpr (NEXT) load_k(kf);
+            wave_lds_sync();  // the previous block's operand reads are done with the slab
+#pragma unroll
+            for (int c = 0; c < NVQ; c++) {
+                const int idx = lane + 64 * c;
+                *reinterpret_cast<f32x4 *>(&vw[idx / (D / 4)][4 * (idx % (D / 4))]) = vr[c];
+            }
+            wave_lds_sync();  // rows staged by other lanes are visible to the operand reads
+            if constexpr (NEXT) load_v(vr);
+            block_pv<D>(o, st, vw, half, l31);
+            if constexpr (NEXT) st = st_next;
+        };
+        for (; kb + ANW < nkb; kb += ANW) step(std::true_type{});
+        step(std::false_type{});
     }
     merge_store<D>(&vslab[0][0][0], o, m_i, l_i, g.o + bi * g.s_ob + h * g.s_oh + (int64_t)qi * g.s_om, qi < n_ctx,
                    D);
@@ -510,11 +534,12 @@ static int attn_launch(AttnArgs g, int64_t batch, int64_t n_heads, int32_t head_
     g.nbh = (int)(batch * n_heads);
     const dim3 grid((unsigned)((int64_t)g.nqg * g.nbh));
     // the fast kernel: exact head_dim, contiguous aligned rows that do not overlap, and every
-    // byte offset of a head (rows up to n_ctx + 32) within 31 bits
+    // byte offset it forms (rows up to n_ctx + 3 * ANW * 32, the loads a few blocks past the
+    // end included) within 31 bits
     const int64_t smax = std::max(g.s_qm, std::max(g.s_kn, g.s_vn));
     const bool fast = (head_dim == 32 || head_dim == 64) && kl == K_VEC_D && g.q_vec && g.v_vec &&
                       g.s_qm >= head_dim && g.s_kn >= head_dim && g.s_vn >= head_dim &&
-                      ((g.n_ctx + 2 * AQG) * smax + head_dim) * 4 < (1LL << 31);
+                      ((g.n_ctx + 3 * ANW * ABN + AQG) * smax + head_dim) * 4 < (1LL << 31);
     if (fast && head_dim == 64) hipLaunchKernelGGL(attn_fwd_fast<64>, grid, dim3(64 * ANW), 0, st, g);
     else if (fast) hipLaunchKernelGGL(attn_fwd_fast<32>, grid, dim3(64 * ANW), 0, st, g);
     else if (head_dim <= 32) launch_d<32>(kl, g, grid, st);

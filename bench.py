@@ -101,7 +101,7 @@ def timed(fn, iters, stream):
     return [s.elapsed_time(e) * 1e-3 for s, e in evs]
 
 
-def timed_graph(fn, iters, reps=3):
+def timed_graph(fn, iters, reps=5):
     """Average duration (s) of fn(i), i = 0..iters-1, launched back to back from a captured HIP
     graph (no host work between launches), timed with HIP events around each replay; the
     median over `reps` replays."""
@@ -116,8 +116,11 @@ def timed_graph(fn, iters, reps=3):
     with torch.cuda.graph(graph):
         for i in range(iters):
             fn(i)
-    graph.replay()
-    torch.cuda.synchronize()
+    # warm: replay for at least 50 ms so clocks have ramped after any idle host phase
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.05:
+        graph.replay()
+        torch.cuda.synchronize()
     out = []
     stream = torch.cuda.current_stream()
     for _ in range(reps):
@@ -176,10 +179,13 @@ def bench_softmax(n, rows=4096, launches=48):
         rt.softmax(ys[i % pairs], xs[i % pairs], n, n, n, rows, block)
 
     avg = timed_graph(step, max(launches, pairs))
+    # the copy ceiling of the same traffic: torch's copy kernel over the same rotated buffers
+    copy = timed_graph(lambda i: ys[i % pairs].copy_(xs[i % pairs]), max(launches, pairs))
     del xs, ys
     torch.cuda.empty_cache()
     return dict(n=n, rows=rows, bytes=pair_bytes, us=round(avg * 1e6, 3), gbs=round(pair_bytes / avg / 1e9, 1),
-                frac=round(pair_bytes / avg / PEAK_HBM, 4), traffic=measured_traffic(f"softmax {rows} x {n}"))
+                frac=round(pair_bytes / avg / PEAK_HBM, 4), copy_gbs=round(pair_bytes / copy / 1e9, 1),
+                traffic=measured_traffic(f"softmax {rows} x {n}"))
 
 
 def bench_attention(launches=32):

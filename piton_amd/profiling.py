@@ -26,11 +26,11 @@ CAL_WRITE = 64 * 2 ** 20 * 4
 # (workload, algorithmic HBM bytes per launch, algorithmic FLOPs per launch)
 BENCH = {
     ("gemm_f32_kernel<0, 0>", 262144): ("matmul 4096^3", 3 * 4096 * 4096 * 4, 2 * 4096 ** 3),
-    ("softmax_rows_kernel<4, 1, true>", 262144): ("softmax 4096 x 1024", 2 * 4 * 4096 * 1024, None),
-    ("softmax_rows_kernel<16, 2, true>", 131072): ("softmax 4096 x 4096", 2 * 4 * 4096 * 4096, None),
-    ("softmax_rows_kernel<8, 2, false>", 131072): ("softmax 4096 x 1823", 2 * 4 * 4096 * 1823, None),
-    ("attn_fwd_kernel_f32<64, 0>", 262144): ("attention 32 x 1024 x 64 causal", 4 * 32 * 1024 * 64 * 4,
-                                             4 * 1024 * 1024 * 64 * 32 // 2),
+    ("softmax_rows_kernel<4, true>", 262144): ("softmax 4096 x 1024", 2 * 4 * 4096 * 1024, None),
+    ("softmax_wg_kernel<4, true>", 1048576): ("softmax 4096 x 4096", 2 * 4 * 4096 * 4096, None),
+    ("softmax_rows_kernel<8, false>", 196608): ("softmax 4096 x 1823", 2 * 4 * 4096 * 1823, None),
+    ("attn_fwd_fast<64>", 262144): ("attention 32 x 1024 x 64 causal", 4 * 32 * 1024 * 64 * 4,
+                                    4 * 1024 * 1024 * 64 * 32 // 2),
 }
 
 

@@ -287,21 +287,88 @@ __global__ __launch_bounds__(GTHREADS) void gemm_f32_kernel(GemmArgs g) {
         }
 }
 
-// First index of the largest of x[r, 0:n] (numpy argmax rule: the first NaN wins).
-__global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int64_t rows, int64_t ld, int64_t n, int32_t *out) {
-    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= rows) return;
+// First index of the largest of x[r, 0:n] (numpy argmax rule: the first NaN wins), one wave
+// per row: each lane scans elements lane, lane + 64, ..., then the (value, index) pairs combine
+// across the wave. The combine (a NaN beats any number, the larger value beats the smaller,
+// equal values and two NaNs go to the lower index) is associative and commutative, so the
+// result is the global first maximum whatever the order.
+__device__ __forceinline__ void argmax_combine(float &v, int &i, float v2, int i2) {
+    const bool n1 = v != v, n2 = v2 != v2;
+    const bool take = (n1 && n2) ? i2 < i : n2 ? true : n1 ? false : (v2 > v || (v2 == v && i2 < i));
+    if (take) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int64_t rows, int64_t ld, int n, int32_t *out) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;  // whole wavefront leaves together
     const float *row = x + r * ld;
-    int32_t best = 0;
-    float bv = row[0];
-    if (bv == bv) {
-        for (int64_t i = 1; i < n; i++) {
-            const float v = row[i];
-            if (v != v) { best = (int32_t)i; break; }
-            if (v > bv) { bv = v; best = (int32_t)i; }
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = lane; i < n; i += 64) argmax_combine(bv, bi, row[i], i);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        const float v2 = __shfl_xor(bv, s);
+        const int i2 = __shfl_xor(bi, s);
+        argmax_combine(bv, bi, v2, i2);
+    }
+    if (lane == 0) out[r] = bi;
+}
+
+// Y = X W (+ bias, ReLU, + residual) for at most 64 rows (a decode step's batch): the big
+// kernel would give such a product a handful of 128 x 128 tiles walking K serially. Here a
+// workgroup owns all the rows and 16 columns (v_mfma_f32_16x16x4f32, four 16-row tiles), its
+// four waves split K, and each lane group of 16 lanes takes a contiguous quarter of its wave's
+// K range (the MFMA's 4-deep k index is permuted that way), so a lane walks consecutive k.
+// The four partial tiles sum in a fixed order through LDS: results do not depend on timing.
+constexpr int SMN = 16;       // columns per workgroup
+constexpr int SMWAVES = 4;    // waves splitting K
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) {
+    __shared__ float part[SMWAVES][4][4][64];  // [wave][row tile][accumulator][lane]
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 4, c16 = lane & 15;
+    const int64_t n0 = (int64_t)blockIdx.x * SMN, n = n0 + c16;
+    const int64_t kq = (g.K + 4 * SMWAVES - 1) / (4 * SMWAVES);  // k per lane group
+    const int64_t kbeg = (int64_t)(wave * 4 + grp) * kq;
+    const bool n_ok = n < g.N;
+    f32x4v acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    const float *wp = g.b + n;
+    for (int64_t s = 0; s < kq; s++) {
+        const int64_t k = kbeg + s;
+        const bool k_ok = k < g.K;
+        const float bv = (k_ok && n_ok) ? wp[k * g.s_bk] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t m = 16 * i + c16;
+            const float av = (k_ok && m < g.M) ? g.a[m * g.s_am + k] : 0.f;
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i], 0, 0, 0);
         }
     }
-    out[r] = best;
+    // accumulator r of row tile i holds row 16*i + 4*grp + r, column n0 + c16
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) part[wave][i][r][lane] = acc[i][r];
+    __syncthreads();
+    const int i = wave;  // thread (wave i, lane) finishes row tile i's accumulators of its lane
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int64_t m = 16 * i + 4 * grp + r;
+        if (m >= g.M || !n_ok) continue;
+        float v = part[0][i][r][lane];
+#pragma unroll
+        for (int w = 1; w < SMWAVES; w++) v += part[w][i][r][lane];
+        if (g.bias) v += g.bias[n];
+        if (g.relu && v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
+        if (g.res) v += g.res[m * g.s_rm + n];
+        g.c[m * g.s_cm + n] = v;
+    }
 }
 
 static int layout_a(const GemmArgs &g) {
@@ -378,8 +445,9 @@ int32_t piton_mi355x_dense(const float *x, const float *w, const float *bias, fl
     rc = launch_gemm(g, st, "dense");
     if (rc) return rc;
     if (argmax_out && M > 0) {
-        hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, st, y, M, N,
-                           (int64_t)n_classes, argmax_out);
+        PITON_REQUIRE((M + 3) / 4 <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "dense: M=%lld too large", (long long)M);
+        hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, y, M, N, n_classes,
+                           argmax_out);
         rc = check_launch("dense argmax");
         if (rc) return rc;
     }
@@ -402,7 +470,14 @@ int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *w, const f
     int rc = require_device();
     if (rc) return rc;
     GemmArgs g{x, w, y, M, N, K, ldx, 1, N, 1, ldy, 1, 1, bias, relu ? 1 : 0, residual, ldr, 0, 0};
-    rc = launch_gemm(g, (hipStream_t)stream, "linear");
+    if (M > 0 && M <= 64) {
+        PITON_REQUIRE((N + SMN - 1) / SMN <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "linear: N=%lld too large", (long long)N);
+        hipLaunchKernelGGL(gemm_small_m_kernel, dim3((unsigned)((N + SMN - 1) / SMN)), dim3(64 * SMWAVES), 0,
+                           (hipStream_t)stream, g);
+        rc = check_launch("linear");
+    } else {
+        rc = launch_gemm(g, (hipStream_t)stream, "linear");
+    }
     if (rc == PITON_OK) clear_error();
     return rc;
 }
@@ -415,8 +490,9 @@ int32_t piton_mi355x_argmax_rows(const float *x, int64_t rows, int64_t ld, int64
     int rc = require_device();
     if (rc) return rc;
     if (rows == 0) return PITON_OK;
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                       x, rows, ld, n, out);
+    PITON_REQUIRE(n <= 0x7FFFFFFF && (rows + 3) / 4 <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "argmax_rows: too large");
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, x,
+                       rows, ld, (int)n, out);
     rc = check_launch("argmax_rows");
     if (rc == PITON_OK) clear_error();
     return rc;

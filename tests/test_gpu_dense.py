@@ -123,6 +123,26 @@ def test_ragged_batches_reuse_buffers():
         np.testing.assert_allclose(logits.cpu().numpy(), ref, rtol=2e-4, atol=2e-4)
 
 
+def test_argmax_rows_wide_rows_across_lanes():
+    """Rows longer than a wave: ties between lanes go to the first index, the first NaN wins
+    wherever it sits, an all -inf row gives 0, row strides are honoured."""
+    rng = np.random.default_rng(9)
+    rows, n, ld = 9, 1000, 1003
+    x = rng.standard_normal((rows, ld)).astype(np.float32)
+    x[1, 700] = x[1, 70] = 50.0            # tie across lanes and passes
+    x[2, 999] = np.nan
+    x[3, 5] = np.nan
+    x[3, 900] = np.nan
+    x[4, :] = -np.inf
+    x[5, 64] = x[5, 128] = x[5, 1] = 99.0  # same lane, three passes
+    x[6, n:] = 1e9                         # past n: never looked at
+    tx = torch.from_numpy(x).cuda()
+    out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    rt.argmax_rows(tx, rows, ld, n, out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), np.argmax(x[:, :n], axis=1))
+
+
 def test_argmax_rows_ties_and_nan():
     x = np.array([[1, 3, 3, 0], [np.nan, 5, np.nan, 1], [2, 2, 2, 2], [-1, -5, np.inf, np.inf]], np.float32)
     tx = torch.from_numpy(x).cuda()

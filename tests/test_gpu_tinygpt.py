@@ -41,6 +41,31 @@ def test_linear_residual_relu_strided():
     assert fp64.rel_fro(y2.cpu().numpy()[:, :N], ref2) <= 1e-6
 
 
+@pytest.mark.parametrize("M,N,K,relu", [(1, 16, 1, False), (5, 17, 7, True), (64, 256, 1024, False),
+                                        (64, 768, 256, True), (33, 100, 300, False), (64, 16, 64, True),
+                                        (63, 1024, 257, False)])
+def test_linear_up_to_64_rows(M, N, K, relu):
+    """Decode-step products (at most 64 rows) take the split-K kernel: strided rows, bias,
+    ReLU and residual, untouched padding, and the same bits on a second run."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    x = rng.standard_normal((M, K + 3)).astype(np.float32)
+    w = rng.standard_normal((K, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    r = rng.standard_normal((M, N + 2)).astype(np.float32)
+    tx, tw, tb, tr = (torch.from_numpy(t).cuda() for t in (x, w, b, r))
+    outs = []
+    for _ in range(2):
+        y = torch.full((M, N + 5), -2.0, device="cuda")
+        rt.linear(tx, K + 3, tw, tb, tr, N + 2, y, N + 5, M, N, K, relu=relu)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    pre = x[:, :K].astype(np.float64) @ w + b
+    ref = (np.maximum(pre, 0) if relu else pre) + r[:, :N]
+    assert fp64.rel_fro(outs[0][:, :N], ref) <= 1e-6
+    assert (outs[0][:, N:] == -2.0).all()
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
 def test_position_major_attention_prefill_and_decode():
     """The decoder's layout: qkv rows t*B + b of 3*D; heads through strides."""
     rng = np.random.default_rng(1)

@@ -470,9 +470,13 @@ static void launch_d(int kl, const AttnArgs &g, dim3 grid, hipStream_t st) {
 }
 
 // One new query per (batch, head) against keys 0 .. n_keys-1 of a cache (the decode step of a
-// KV-cached decoder): one wavefront per (batch, head); lanes score keys j = lane, lane + 64, ...
-// into LDS, two DPP reductions give the max and the sum, then lane d accumulates
-// sum_j p_j V[j][d] with coalesced V rows.
+// KV-cached decoder): one 256-thread workgroup per (batch, head).
+//   * scores: D/16 consecutive lanes share a key, 16 head dims each (four float4 loads of the
+//     key row), and add their partial dot products with lane exchanges; the scores go to LDS;
+//   * the maximum and the sum of exps over the keys reduce across the workgroup (DPP within a
+//     wave, then the four wave results through LDS);
+//   * P V: thread (g, d) sums p_j V[j][d] over the keys j = g mod 256/D with coalesced V rows;
+//     the 256/D partial sums of a dim add in a fixed order.
 constexpr int kMaxDecodeKeys = 8192;
 
 struct DecodeArgs {
@@ -483,45 +487,80 @@ struct DecodeArgs {
     int n_keys, n_heads, head_dim;
 };
 
-template <int D>
-__global__ __launch_bounds__(64) void attn_decode_kernel(DecodeArgs g) {
+template <class Op>
+__device__ __forceinline__ float block_reduce4(float v, Op op, float *red) {
+    v = wave_reduce(v, op);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return op(op(red[0], red[1]), op(red[2], red[3]));
+}
+
+template <int D, bool VEC>
+__global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs g) {
     __shared__ float p[kMaxDecodeKeys];
-    const int lane = threadIdx.x;
+    __shared__ float red[8];
+    __shared__ float part[256];
+    constexpr int TPK = D / 16, KPP = 256 / TPK, KG = 256 / D;
+    const int t = threadIdx.x;
     const int64_t bh = blockIdx.x, b = bh / g.n_heads, h = bh % g.n_heads;
     const float *qp = g.q + b * g.s_qb + h * g.s_qh;
     const float *kp = g.k + b * g.s_kb + h * g.s_kh;
     const float *vp = g.v + b * g.s_vb + h * g.s_vh;
-    float q[D];
+    const int n_keys = g.n_keys, head_dim = g.head_dim;
+
+    // this lane's 16 dims of the query (scaled), and of each key it scores
+    const int sub = t % TPK, kslot = t / TPK, d0 = 16 * sub;
+    const bool dims_ok = d0 < head_dim;  // head_dim is a multiple of 16
+    float q16[16];
 #pragma unroll
-    for (int d = 0; d < D; d++) q[d] = d < g.head_dim ? qp[d] * g.scale : 0.f;
+    for (int i = 0; i < 16; i++) q16[i] = dims_ok ? qp[d0 + i] * g.scale : 0.f;
     float mloc = -INFINITY;
-    for (int j = lane; j < g.n_keys; j += 64) {
-        const float *kr = kp + (int64_t)j * g.s_kn;
-        float s = 0.f;
+    for (int j0 = 0; j0 < n_keys; j0 += KPP) {
+        const int j = j0 + kslot;
+        float sc = 0.f;
+        if (j < n_keys && dims_ok) {
+            const float *kr = kp + (int64_t)j * g.s_kn + d0;
 #pragma unroll
-        for (int d = 0; d < D; d++)
-            if (d < g.head_dim) s = fmaf(q[d], kr[d], s);
-        p[j] = s;
-        mloc = fmaxf(mloc, s);
+            for (int c = 0; c < 4; c++) {
+                float4 f;
+                if constexpr (VEC) f = *reinterpret_cast<const float4 *>(kr + 4 * c);
+                else f = make_float4(kr[4 * c], kr[4 * c + 1], kr[4 * c + 2], kr[4 * c + 3]);
+                sc = fmaf(q16[4 * c], f.x, sc);
+                sc = fmaf(q16[4 * c + 1], f.y, sc);
+                sc = fmaf(q16[4 * c + 2], f.z, sc);
+                sc = fmaf(q16[4 * c + 3], f.w, sc);
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < TPK; o <<= 1) sc += __shfl_xor(sc, o);  // the key's TPK lanes are consecutive
+        if (j < n_keys) {
+            if (sub == 0) p[j] = sc;
+            mloc = fmaxf(mloc, sc);
+        }
     }
-    const float m = wave_reduce(mloc, MaxOp());
+    const float m = block_reduce4(mloc, MaxOp(), red);  // its barrier also publishes the scores
     float lsum = 0.f;
-    for (int j = lane; j < g.n_keys; j += 64) {
+    for (int j = t; j < n_keys; j += 256) {
         const float e = __builtin_amdgcn_exp2f(p[j] - m);
         p[j] = e;
         lsum += e;
     }
-    const float inv = 1.0f / wave_reduce(lsum, SumOp());
+    const float inv = 1.0f / block_reduce4(lsum, SumOp(), red + 4);  // and publishes the exps
+
+    const int d = t % D, kg = t / D;
+    float acc = 0.f;
+    if (d < head_dim) {
+        const float *vc = vp + d;
+#pragma unroll 4
+        for (int j = kg; j < n_keys; j += KG) acc = fmaf(p[j], vc[(int64_t)j * g.s_vn], acc);
+    }
+    part[t] = acc;
     __syncthreads();
-    float *op = g.o + b * g.s_ob + h * g.s_oh;
+    if (t < D && t < head_dim) {
+        float v = part[t];
 #pragma unroll
-    for (int d0 = 0; d0 < D; d0 += 64) {
-        const int d = d0 + lane;
-        if (d < g.head_dim) {
-            float acc = 0.f;
-            for (int j = 0; j < g.n_keys; j++) acc = fmaf(p[j], vp[(int64_t)j * g.s_vn + d], acc);
-            op[d] = acc * inv;
-        }
+        for (int w = 1; w < KG; w++) v += part[w * D + t];
+        g.o[b * g.s_ob + h * g.s_oh + t] = v * inv;
     }
 }
 
@@ -625,10 +664,17 @@ int32_t piton_mi355x_attn_decode(const float *q, const float *k, const float *v,
     DecodeArgs g{q, k, v, out, sm_scale * 1.44269504088896341f, stride_qb, stride_qh, stride_kb, stride_kh, stride_kn,
                  stride_vb, stride_vh, stride_vn, stride_ob, stride_oh, (int)n_keys, (int)n_heads, head_dim};
     hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((unsigned)(batch * n_heads)), block(64);
-    if (head_dim <= 32) hipLaunchKernelGGL(attn_decode_kernel<32>, grid, block, 0, st, g);
-    else if (head_dim == 64) hipLaunchKernelGGL(attn_decode_kernel<64>, grid, block, 0, st, g);
-    else hipLaunchKernelGGL(attn_decode_kernel<128>, grid, block, 0, st, g);
+    const dim3 grid((unsigned)(batch * n_heads)), block(256);
+    const bool vec = aligned16(k) && stride_kn % 4 == 0 && stride_kh % 4 == 0 && stride_kb % 4 == 0;
+#define PITON_DEC(D)                                                                                                \
+    do {                                                                                                            \
+        if (vec) hipLaunchKernelGGL((attn_decode_kernel<D, true>), grid, block, 0, st, g);                          \
+        else hipLaunchKernelGGL((attn_decode_kernel<D, false>), grid, block, 0, st, g);                             \
+    } while (0)
+    if (head_dim <= 32) PITON_DEC(32);
+    else if (head_dim == 64) PITON_DEC(64);
+    else PITON_DEC(128);
+#undef PITON_DEC
     rc = check_launch("attn_decode");
     if (rc == PITON_OK) clear_error();
     return rc;

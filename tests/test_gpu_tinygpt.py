@@ -89,6 +89,29 @@ def test_position_major_attention_prefill_and_decode():
     assert fp64.rel_fro(got_dec, ref[:, :, -1]) <= 1e-5
 
 
+@pytest.mark.parametrize("dh,n_keys,pad", [(16, 3, 0), (32, 1, 0), (64, 257, 0), (128, 1000, 0), (64, 300, 1),
+                                           (128, 8192, 0)])
+def test_decode_attention_head_dims_and_long_caches(dh, n_keys, pad):
+    """One query per (batch, head) against n_keys cached keys, [B, H, N, Dh] caches with a row
+    padding of `pad` floats (pad = 1 takes the scalar-load path), up to the 8192-key limit."""
+    rng = np.random.default_rng(dh + n_keys)
+    B, H = 2, 3
+    row = dh + pad
+    q = rng.standard_normal((B, H, dh)).astype(np.float32)
+    k = rng.standard_normal((B, H, n_keys, row)).astype(np.float32)
+    v = rng.standard_normal((B, H, n_keys, row)).astype(np.float32)
+    tq, tk, tv = (torch.from_numpy(t).cuda() for t in (q, k, v))
+    out = torch.full((B, H, dh + 2), -9.0, device="cuda")
+    scale = 1.0 / np.sqrt(dh)
+    rt.attn_decode(tq, tk, tv, out, scale, H * dh, dh, H * n_keys * row, n_keys * row, row, H * n_keys * row,
+                   n_keys * row, row, H * (dh + 2), dh + 2, n_keys, B, H, dh)
+    torch.cuda.synchronize()
+    ref = fp64.attention_reference(q[:, :, None, :], k[..., :dh], v[..., :dh], False, scale)[:, :, 0]
+    got = out.cpu().numpy()
+    assert fp64.rel_fro(got[..., :dh], ref) <= 1e-5
+    assert (got[..., dh:] == -9.0).all()
+
+
 def test_strided_embedding_and_bad_ids():
     rng = np.random.default_rng(2)
     B, T, D, V = 3, 7, 16, 11

@@ -226,7 +226,8 @@ def bench_mlp(reps=3):
 
 def bench_tinygpt():
     """TinyGPT greedy decoding: 64 prompts x 32 tokens, 128 new tokens each, K/V cache; the
-    whole generate() call (host loop and launches included)."""
+    whole timed generate() call: prompt copy-in, the decode (prefill and 127 steps) replayed
+    from the HIP graph the warm-up call captured, token copy-out."""
     import torch
 
     from piton_amd import tinygpt
@@ -239,7 +240,8 @@ def bench_tinygpt():
     model.generate(prompts, 128)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    return dict(sequences=64, prompt=32, new_tokens=128, s=round(dt, 4), tokens_per_s=round(64 * 128 / dt, 1))
+    return dict(sequences=64, prompt=32, new_tokens=128, s=round(dt, 4), tokens_per_s=round(64 * 128 / dt, 1),
+                graph=True)
 
 
 def cpu_baseline(a, b, budget_s=10.0):

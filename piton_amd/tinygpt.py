@@ -88,6 +88,7 @@ class TinyGPT:
         self.logits = torch.empty((batch, V), device=device)
         self.tokens = torch.zeros((C + 1) * batch, dtype=torch.int32, device=device)  # row t*B + b
         self.err = torch.zeros(1, dtype=torch.int32, device=device)
+        self._graphs = {}  # (T0, steps, kv_cache) -> captured decode
 
     # -- one forward over positions [p0, p1) ---------------------------------------------------
 
@@ -125,21 +126,45 @@ class TinyGPT:
         rt.linear(self.h[last:last + B], D, self.w["lm"], None, None, 0, self.logits, V, B, V, D)
         rt.argmax_rows(self.logits, B, V, V, self.tokens[p1 * B:(p1 + 1) * B])
 
-    def generate(self, prompts, steps: int, kv_cache: bool = True) -> np.ndarray:
-        """Greedy continuation of int32 prompts [B, T0] by `steps` tokens; returns [B, T0 + steps]."""
-        prompts = np.ascontiguousarray(prompts, np.int32)
-        B, T0 = prompts.shape
-        if B != self.B or T0 < 1 or T0 + steps > self.cfg.context:
-            raise ValueError(f"prompts {prompts.shape} and {steps} steps do not fit batch {self.B}, "
-                             f"context {self.cfg.context}")
-        self.tokens[:T0 * B].copy_(torch.from_numpy(prompts.T.copy().reshape(-1)))
-        self.err.zero_()
+    def _decode(self, T0: int, steps: int, kv_cache: bool):
         self._forward(0, T0)
         for t in range(T0, T0 + steps - 1):
             if kv_cache:
                 self._forward(t, t + 1)
             else:
                 self._forward(0, t + 1)
+
+    def generate(self, prompts, steps: int, kv_cache: bool = True, graph: bool | None = None) -> np.ndarray:
+        """Greedy continuation of int32 prompts [B, T0] by `steps` tokens; returns [B, T0 + steps].
+
+        graph (default: on a GPU): the whole decode (prefill and every step, positions baked in)
+        is captured once per (T0, steps, kv_cache) as a HIP graph and replayed on later calls,
+        so a step costs no host launches. The capture call runs the decode eagerly first (its
+        tokens are the ones returned) and then records it; the prompts are copied in before
+        every replay."""
+        prompts = np.ascontiguousarray(prompts, np.int32)
+        B, T0 = prompts.shape
+        if B != self.B or T0 < 1 or T0 + steps > self.cfg.context:
+            raise ValueError(f"prompts {prompts.shape} and {steps} steps do not fit batch {self.B}, "
+                             f"context {self.cfg.context}")
+        use_graph = self.x.is_cuda if graph is None else graph
+        self.tokens[:T0 * B].copy_(torch.from_numpy(prompts.T.copy().reshape(-1)))
+        self.err.zero_()
+        key = (T0, steps, kv_cache)
+        if use_graph and key in self._graphs:
+            self._graphs[key].replay()
+        elif use_graph:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self._decode(T0, steps, kv_cache)
+            torch.cuda.current_stream().wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._decode(T0, steps, kv_cache)
+            self._graphs[key] = g
+        else:
+            self._decode(T0, steps, kv_cache)
         out = self.tokens[:(T0 + steps) * B].view(T0 + steps, B).t().contiguous().cpu().numpy()
         if int(self.err.item()):
             raise RuntimeError("a token id outside the vocabulary reached the embedding")

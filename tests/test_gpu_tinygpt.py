@@ -179,3 +179,21 @@ def test_config_greedy_64x128_matches_float64():
     for seq, pos, margin in div:
         assert margin < TAU, (seq, pos, margin)
     assert len(div) <= 2
+
+
+def test_graph_replays_equal_eager_decoding():
+    """The captured decode replayed several times, with other prompts, eager decodes and
+    synchronisations between the replays: every replay's tokens equal the eager run's."""
+    w = tinygpt.init_weights(seed=0)
+    model = tinygpt.TinyGPT(w, batch=16)
+    sets = [tinygpt.seeded_prompts(batch=16, length=12, seed=s) for s in (7, 8, 9)]
+    first = model.generate(sets[0], 20)          # runs eagerly, then captures
+    np.testing.assert_array_equal(first, model.generate(sets[0], 20, graph=False))
+    for i in range(5):
+        p = sets[i % 3]
+        replay = model.generate(p, 20)            # replays the graph
+        torch.cuda.synchronize()
+        eager = model.generate(p, 20, graph=False)
+        np.testing.assert_array_equal(replay, eager)
+        np.testing.assert_array_equal(replay[:, :12], p)
+    assert len(model._graphs) == 1

@@ -311,8 +311,7 @@ def main():
                      "kernel_us": round(avg * 1e6, 2)},
         "device": {k: info[k] for k in ("arch", "cu_count", "max_clock_khz", "hbm_bytes")},
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(mm["a"], mm["b"])
+    a_host, b_host = (mm["a"].cpu(), mm["b"].cpu()) if not args.no_cpu else (None, None)
     del mm
     torch.cuda.empty_cache()
     if not args.no_extras:
@@ -320,6 +319,8 @@ def main():
         line["attention"] = bench_attention()
         line["mlp"] = bench_mlp()
         line["tinygpt"] = bench_tinygpt()
+    if not args.no_cpu:  # last: the GPU idles while the host cores work
+        line["cpu_baseline"] = cpu_baseline(a_host, b_host)
     print(json.dumps(line))
 
 

@@ -152,6 +152,46 @@ PITON_API int32_t piton_mi355x_attn_decode(const float *q, const float *k, const
                                  int64_t stride_oh, int64_t n_keys, int64_t batch, int64_t n_heads,
                                  int32_t head_dim, void *stream);
 
+/* ---- the perf suite's primitives (perf/suite.py:323-351): elementwise over n elements ---- */
+
+/* out = x. Replaces copy_kernel (examples/primitive_kernels.py:12-17). */
+PITON_API int32_t piton_mi355x_copy(const float *x, float *out, int64_t n, void *stream);
+
+/* out = x * y. Replaces mul_kernel (examples/elementwise.py:5-9). */
+PITON_API int32_t piton_mi355x_mul(const float *x, const float *y, float *out, int64_t n, void *stream);
+
+/* out = x * alpha + y. Replaces fma_kernel (examples/primitive_kernels.py:20-27). */
+PITON_API int32_t piton_mi355x_fma(const float *x, const float *y, float *out, int64_t n, float alpha,
+                                   void *stream);
+
+/* out = x > 0 ? x * alpha : 0. Replaces scaled_relu_kernel (examples/kernels.py:79-85). */
+PITON_API int32_t piton_mi355x_scaled_relu(const float *x, float *out, int64_t n, float alpha, void *stream);
+
+/* out = f(x) for OP 0 exp2, 1 log2, 2 1/x, 3 1/sqrt, 4 exp, 5 sqrt. Replaces sfu_kernel
+ * (examples/sfu_tests.py:5-22). */
+PITON_API int32_t piton_mi355x_sfu(const float *x, float *out, int64_t n, int32_t op, void *stream);
+
+/* out = ln(x). Replaces log_kernel (examples/primitive_kernels.py:70-76). */
+PITON_API int32_t piton_mi355x_log(const float *x, float *out, int64_t n, void *stream);
+
+/* q = x / y and r = x % y on int32, truncating toward zero as C does (y = 0 gives an unspecified
+ * value, no trap). Replaces idiv_kernel (examples/primitive_kernels.py:30-38). */
+PITON_API int32_t piton_mi355x_idiv(const int32_t *x, const int32_t *y, int32_t *q, int32_t *r, int64_t n,
+                                    void *stream);
+
+/* out[r] = sum (or max, starting from -FLT_MAX) of x[r, 0:n_cols], rows of stride `stride`.
+ * Replace row_sum_kernel (examples/kernels.py:88-96) and row_max_kernel
+ * (examples/primitive_kernels.py:41-50). */
+PITON_API int32_t piton_mi355x_row_sum(const float *x, float *out, int64_t rows, int64_t n_cols, int64_t stride,
+                                       void *stream);
+PITON_API int32_t piton_mi355x_row_max(const float *x, float *out, int64_t rows, int64_t n_cols, int64_t stride,
+                                       void *stream);
+
+/* out[c, r] = x[r, c] for r < n_rows, c < n_cols. Replaces transpose_kernel
+ * (examples/primitive_kernels.py:53-67). */
+PITON_API int32_t piton_mi355x_transpose(const float *x, float *out, int64_t n_rows, int64_t n_cols,
+                                         int64_t stride_x, int64_t stride_out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

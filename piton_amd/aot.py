@@ -85,6 +85,37 @@ KERNELS = {
 }
 
 
+def _map_spec(entry, ptrs, scalars=()):
+    return dict(params=(*ptrs, "n", *scalars, "BLOCK") if "OP" not in scalars else (*ptrs, "n", "OP", "BLOCK"),
+                entry=entry, call=(*[f"{{{p}}}" for p in ptrs], "{n}", *[f"{{{s}}}" for s in scalars]),
+                grid=(cdiv_c("{n}", "{BLOCK}"), "1", "1"))
+
+
+def _row_spec(entry):
+    return dict(params=("x_ptr", "out_ptr", "n_cols", "stride", "BLOCK_M", "BLOCK_N"), entry=entry,
+                call=("{x_ptr}", "{out_ptr}", "(long long)gx * ({BLOCK_M})",
+                      cdiv_c("{n_cols}", "{BLOCK_N}") + " * ({BLOCK_N})", "{stride}"),
+                grid=(None, "1", "1"))
+
+
+KERNELS.update({
+    "copy_kernel": _map_spec("piton_mi355x_copy", ("x_ptr", "out_ptr")),
+    "mul_kernel": _map_spec("piton_mi355x_mul", ("x_ptr", "y_ptr", "out_ptr")),
+    "fma_kernel": _map_spec("piton_mi355x_fma", ("x_ptr", "y_ptr", "out_ptr"), ("alpha",)),
+    "scaled_relu_kernel": _map_spec("piton_mi355x_scaled_relu", ("x_ptr", "out_ptr"), ("alpha",)),
+    "sfu_kernel": _map_spec("piton_mi355x_sfu", ("x_ptr", "out_ptr"), ("OP",)),
+    "log_kernel": _map_spec("piton_mi355x_log", ("x_ptr", "out_ptr")),
+    "idiv_kernel": _map_spec("piton_mi355x_idiv", ("x_ptr", "y_ptr", "q_ptr", "r_ptr")),
+    "row_sum_kernel": _row_spec("piton_mi355x_row_sum"),
+    "row_max_kernel": _row_spec("piton_mi355x_row_max"),
+    "transpose_kernel": dict(
+        params=("x_ptr", "out_ptr", "n_rows", "n_cols", "stride_x", "stride_out", "BLOCK_M", "BLOCK_N"),
+        entry="piton_mi355x_transpose",
+        call=("{x_ptr}", "{out_ptr}", "{n_rows}", "{n_cols}", "{stride_x}", "{stride_out}"),
+        grid=(cdiv_c("{n_rows}", "{BLOCK_M}") + " * " + cdiv_c("{n_cols}", "{BLOCK_N}"), "1", "1")),
+})
+
+
 def _parse_kv(text: str) -> dict:
     out = {}
     for item in filter(None, (t.strip() for t in text.split(","))):

@@ -1,0 +1,244 @@
+// The perf suite's primitives (perf/suite.py:323-351) on gfx950: copy, mul, fma, scaled_relu,
+// the special functions of sfu_kernel (examples/sfu_tests.py:6-22) and log, exact int32 //
+// and %, row sums and maxima, and the tiled transpose (examples/primitive_kernels.py:13-76,
+// examples/kernels.py:80-96, examples/elementwise.py:6-9).
+//
+// Every one of them moves more bytes than it computes, so each is shaped for HBM:
+//   * elementwise: one 16-byte vector per thread on an exact grid (many short workgroups keep
+//     reads and writes interleaved), nontemporal loads and stores, a scalar tail for n % 4;
+//   * special functions use the device math library (expf, exp2f, logf, log2f, sqrtf) and an
+//     IEEE division for the reciprocal and 1/sqrt: within a few ulp, inside the suite's 4e-6;
+//   * row reductions: one wavefront per row, float4 loads along the row, DPP reductions;
+//   * transpose: 64 x 64 tiles through LDS (row stride 65), so reads and writes are both
+//     coalesced 256-byte rows.
+#include <math.h>
+
+#include "common.h"
+
+namespace piton {
+
+struct CopyOp { __device__ float operator()(float x, float, float) const { return x; } };
+struct MulOp { __device__ float operator()(float x, float y, float) const { return x * y; } };
+struct FmaOp { __device__ float operator()(float x, float y, float a) const { return x * a + y; } };
+struct ScaledReluOp { __device__ float operator()(float x, float, float a) const { return x > 0.f ? x * a : 0.f; } };
+struct Exp2Op { __device__ float operator()(float x, float, float) const { return exp2f(x); } };
+struct Log2Op { __device__ float operator()(float x, float, float) const { return log2f(x); } };
+struct RecipOp { __device__ float operator()(float x, float, float) const { return 1.0f / x; } };
+struct RsqrtOp { __device__ float operator()(float x, float, float) const { return 1.0f / sqrtf(x); } };
+struct ExpOp { __device__ float operator()(float x, float, float) const { return expf(x); } };
+struct SqrtOp { __device__ float operator()(float x, float, float) const { return sqrtf(x); } };
+struct LogOp { __device__ float operator()(float x, float, float) const { return logf(x); } };
+
+// out[i] = op(x[i], y[i], alpha) for i < n; y may be null for one-input ops
+template <class Op, bool TWO>
+__global__ __launch_bounds__(256) void map_vec4_kernel(const f32x4 *x, const f32x4 *y, f32x4 *out, int64_t n4,
+                                                       float alpha) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const f32x4 a = __builtin_nontemporal_load(x + i);
+    const f32x4 b = TWO ? __builtin_nontemporal_load(y + i) : a;
+    Op op;
+    __builtin_nontemporal_store(f32x4{op(a.x, b.x, alpha), op(a.y, b.y, alpha), op(a.z, b.z, alpha),
+                                      op(a.w, b.w, alpha)}, out + i);
+}
+
+template <class Op, bool TWO>
+__global__ __launch_bounds__(256) void map_scalar_kernel(const float *x, const float *y, float *out, int64_t begin,
+                                                         int64_t n, float alpha) {
+    const int64_t i = begin + (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    Op op;
+    out[i] = op(x[i], TWO ? y[i] : 0.f, alpha);
+}
+
+template <class Op, bool TWO>
+static int launch_map(const float *x, const float *y, float *out, int64_t n, float alpha, hipStream_t st,
+                      const char *what) {
+    if (n == 0) return PITON_OK;
+    const bool vec = aligned16(x) && aligned16(out) && (!TWO || aligned16(y));
+    const int64_t n4 = vec ? n / 4 : 0;
+    PITON_REQUIRE((n4 + 255) / 256 <= 0x7FFFFFFF && (n - 4 * n4 + 255) / 256 <= 0x7FFFFFFF, PITON_EUNSUPPORTED,
+                  "%s: n=%lld too large", what, (long long)n);
+    if (n4 > 0)
+        hipLaunchKernelGGL((map_vec4_kernel<Op, TWO>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                           reinterpret_cast<const f32x4 *>(x), reinterpret_cast<const f32x4 *>(y),
+                           reinterpret_cast<f32x4 *>(out), n4, alpha);
+    if (4 * n4 < n)
+        hipLaunchKernelGGL((map_scalar_kernel<Op, TWO>), dim3((unsigned)((n - 4 * n4 + 255) / 256)), dim3(256), 0,
+                           st, x, y, out, 4 * n4, n, alpha);
+    return check_launch(what);
+}
+
+// C-style (truncating) quotient and remainder: q = trunc(x / y), r = x - q y
+__global__ __launch_bounds__(256) void idiv_kernel(const int32_t *x, const int32_t *y, int32_t *q, int32_t *r,
+                                                   int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int32_t a = x[i], b = y[i];
+    const int32_t qq = a / b;
+    q[i] = qq;
+    r[i] = a - qq * b;
+}
+
+// out[r] = sum / max of x[r, 0:n_cols] (row stride `stride`), one wave per row
+template <bool MAX>
+__global__ __launch_bounds__(256) void row_reduce_kernel(const float *x, float *out, int64_t rows, int64_t n_cols,
+                                                         int64_t stride, int vec) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;  // whole wavefront leaves together
+    const float *p = x + row * stride;
+    float acc = MAX ? -3.4028234663852886e+38f : 0.f;
+    int64_t c0 = 0;
+    if (vec) {
+        const int64_t n4 = n_cols / 4;
+        for (int64_t i = lane; i < n4; i += 64) {
+            const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p) + i);
+            acc = MAX ? fmaxf(acc, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w))) : acc + ((v.x + v.y) + (v.z + v.w));
+        }
+        c0 = 4 * n4;
+    }
+    for (int64_t c = c0 + lane; c < n_cols; c += 64) acc = MAX ? fmaxf(acc, p[c]) : acc + p[c];
+    acc = MAX ? wave_reduce(acc, MaxOp()) : wave_reduce(acc, SumOp());
+    if (lane == 0) out[row] = acc;
+}
+
+// out[c, r] = x[r, c]: 64 x 64 tiles, 256 threads, through LDS
+__global__ __launch_bounds__(256) void transpose_kernel(const float *x, float *out, int64_t n_rows, int64_t n_cols,
+                                                        int64_t stride_x, int64_t stride_out, int64_t tiles_n) {
+    __shared__ float tile[64][65];
+    const int64_t tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+    const int64_t r0 = tm * 64, c0 = tn * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int rr = ty + 4 * k;
+        const int64_t r = r0 + rr, c = c0 + tx;
+        if (r < n_rows && c < n_cols) tile[rr][tx] = x[r * stride_x + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int cc = ty + 4 * k;
+        const int64_t c = c0 + cc, r = r0 + tx;
+        if (c < n_cols && r < n_rows) out[c * stride_out + r] = tile[tx][cc];
+    }
+}
+
+}  // namespace piton
+
+using namespace piton;
+
+#define PITON_MAP_ENTRY_CHECKS(what, two)                                                                   \
+    PITON_REQUIRE(n >= 0, PITON_EINVAL, what ": negative n=%lld", (long long)n);                            \
+    PITON_REQUIRE(n == 0 || (x && out && (!(two) || y)), PITON_EINVAL, what ": null pointer");              \
+    PITON_REQUIRE(aligned4(x) && aligned4(out) && aligned4(y), PITON_EINVAL, what ": pointers must be 4-byte aligned"); \
+    int rc = require_device();                                                                              \
+    if (rc) return rc
+
+static int32_t finish(int rc) {
+    if (rc == PITON_OK) clear_error();
+    return rc;
+}
+
+extern "C" {
+
+int32_t piton_mi355x_copy(const float *x, float *out, int64_t n, void *stream) {
+    const float *y = nullptr;
+    PITON_MAP_ENTRY_CHECKS("copy", false);
+    return finish(launch_map<CopyOp, false>(x, nullptr, out, n, 0.f, (hipStream_t)stream, "copy"));
+}
+
+int32_t piton_mi355x_mul(const float *x, const float *y, float *out, int64_t n, void *stream) {
+    PITON_MAP_ENTRY_CHECKS("mul", true);
+    return finish(launch_map<MulOp, true>(x, y, out, n, 0.f, (hipStream_t)stream, "mul"));
+}
+
+int32_t piton_mi355x_fma(const float *x, const float *y, float *out, int64_t n, float alpha, void *stream) {
+    PITON_MAP_ENTRY_CHECKS("fma", true);
+    return finish(launch_map<FmaOp, true>(x, y, out, n, alpha, (hipStream_t)stream, "fma"));
+}
+
+int32_t piton_mi355x_scaled_relu(const float *x, float *out, int64_t n, float alpha, void *stream) {
+    const float *y = nullptr;
+    PITON_MAP_ENTRY_CHECKS("scaled_relu", false);
+    return finish(launch_map<ScaledReluOp, false>(x, nullptr, out, n, alpha, (hipStream_t)stream, "scaled_relu"));
+}
+
+int32_t piton_mi355x_sfu(const float *x, float *out, int64_t n, int32_t op, void *stream) {
+    const float *y = nullptr;
+    PITON_REQUIRE(op >= 0 && op <= 5, PITON_EINVAL, "sfu: OP %d not in 0..5", op);
+    PITON_MAP_ENTRY_CHECKS("sfu", false);
+    hipStream_t st = (hipStream_t)stream;
+    switch (op) {
+        case 0: return finish(launch_map<Exp2Op, false>(x, nullptr, out, n, 0.f, st, "sfu exp2"));
+        case 1: return finish(launch_map<Log2Op, false>(x, nullptr, out, n, 0.f, st, "sfu log2"));
+        case 2: return finish(launch_map<RecipOp, false>(x, nullptr, out, n, 0.f, st, "sfu recip"));
+        case 3: return finish(launch_map<RsqrtOp, false>(x, nullptr, out, n, 0.f, st, "sfu rsqrt"));
+        case 4: return finish(launch_map<ExpOp, false>(x, nullptr, out, n, 0.f, st, "sfu exp"));
+        default: return finish(launch_map<SqrtOp, false>(x, nullptr, out, n, 0.f, st, "sfu sqrt"));
+    }
+}
+
+int32_t piton_mi355x_log(const float *x, float *out, int64_t n, void *stream) {
+    const float *y = nullptr;
+    PITON_MAP_ENTRY_CHECKS("log", false);
+    return finish(launch_map<LogOp, false>(x, nullptr, out, n, 0.f, (hipStream_t)stream, "log"));
+}
+
+int32_t piton_mi355x_idiv(const int32_t *x, const int32_t *y, int32_t *q, int32_t *r, int64_t n, void *stream) {
+    PITON_REQUIRE(n >= 0, PITON_EINVAL, "idiv: negative n=%lld", (long long)n);
+    PITON_REQUIRE(n == 0 || (x && y && q && r), PITON_EINVAL, "idiv: null pointer");
+    PITON_REQUIRE((n + 255) / 256 <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "idiv: n=%lld too large", (long long)n);
+    int rc = require_device();
+    if (rc) return rc;
+    if (n == 0) return PITON_OK;
+    hipLaunchKernelGGL(idiv_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, y, q, r,
+                       n);
+    return finish(check_launch("idiv"));
+}
+
+static int32_t row_reduce_entry(bool is_max, const float *x, float *out, int64_t rows, int64_t n_cols, int64_t stride,
+                                void *stream) {
+    const char *what = is_max ? "row_max" : "row_sum";
+    PITON_REQUIRE(rows >= 0 && n_cols >= 0 && (rows <= 1 || stride >= n_cols), PITON_EINVAL,
+                  "%s: rows=%lld n_cols=%lld stride=%lld", what, (long long)rows, (long long)n_cols, (long long)stride);
+    PITON_REQUIRE(rows == 0 || (x && out), PITON_EINVAL, "%s: null pointer", what);
+    PITON_REQUIRE((rows + 3) / 4 <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "%s: too many rows", what);
+    int rc = require_device();
+    if (rc) return rc;
+    if (rows == 0) return PITON_OK;
+    const int vec = aligned16(x) && (stride % 4 == 0 || rows == 1);
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    if (is_max) hipLaunchKernelGGL(row_reduce_kernel<true>, grid, block, 0, (hipStream_t)stream, x, out, rows, n_cols, stride, vec);
+    else hipLaunchKernelGGL(row_reduce_kernel<false>, grid, block, 0, (hipStream_t)stream, x, out, rows, n_cols, stride, vec);
+    return finish(check_launch(what));
+}
+
+int32_t piton_mi355x_row_sum(const float *x, float *out, int64_t rows, int64_t n_cols, int64_t stride, void *stream) {
+    return row_reduce_entry(false, x, out, rows, n_cols, stride, stream);
+}
+
+int32_t piton_mi355x_row_max(const float *x, float *out, int64_t rows, int64_t n_cols, int64_t stride, void *stream) {
+    return row_reduce_entry(true, x, out, rows, n_cols, stride, stream);
+}
+
+int32_t piton_mi355x_transpose(const float *x, float *out, int64_t n_rows, int64_t n_cols, int64_t stride_x,
+                               int64_t stride_out, void *stream) {
+    PITON_REQUIRE(n_rows >= 0 && n_cols >= 0, PITON_EINVAL, "transpose: negative size");
+    PITON_REQUIRE(n_rows <= 1 || stride_x >= n_cols, PITON_EINVAL, "transpose: stride_x %lld < n_cols %lld",
+                  (long long)stride_x, (long long)n_cols);
+    PITON_REQUIRE(n_cols <= 1 || stride_out >= n_rows, PITON_EINVAL, "transpose: stride_out %lld < n_rows %lld",
+                  (long long)stride_out, (long long)n_rows);
+    PITON_REQUIRE(n_rows == 0 || n_cols == 0 || (x && out), PITON_EINVAL, "transpose: null pointer");
+    const int64_t tiles_m = (n_rows + 63) / 64, tiles_n = (n_cols + 63) / 64;
+    PITON_REQUIRE(tiles_m * tiles_n <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "transpose: too large");
+    int rc = require_device();
+    if (rc) return rc;
+    if (n_rows == 0 || n_cols == 0) return PITON_OK;
+    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, (hipStream_t)stream, x,
+                       out, n_rows, n_cols, stride_x, stride_out, tiles_n);
+    return finish(check_launch("transpose"));
+}
+
+}  // extern "C"

@@ -162,6 +162,32 @@ def _plan_layernorm(a, grid):
     return "layernorm", (Arr("x_ptr"), Arr("out_ptr"), min(int(a["n"]), block), float(a["eps"]), g[0], block)
 
 
+def _plan_map(entry, ptrs, scalars=()):
+    """An elementwise primitive: grid (cdiv(n, BLOCK),), arguments (pointers..., n, scalars...)."""
+    def plan(a, grid):
+        n = int(a["n"])
+        _expect_grid(entry + "_kernel", grid, (cdiv(n, a["BLOCK"]),))
+        return entry, (*[Arr(p) for p in ptrs], n, *[conv(a[s]) for s, conv in scalars])
+    return plan
+
+
+def _plan_row_reduce(entry):
+    def plan(a, grid):
+        g = _grid3(grid)
+        if g[1] != 1 or g[2] != 1:
+            raise ValueError(f"{entry}_kernel: grid {tuple(grid)} must be (rows / BLOCK_M,)")
+        # the reference reads whole BLOCK_N chunks of each row, unmasked (kernels.py:92-95)
+        cols = cdiv(int(a["n_cols"]), a["BLOCK_N"]) * int(a["BLOCK_N"])
+        return entry, (Arr("x_ptr"), Arr("out_ptr"), g[0] * int(a["BLOCK_M"]), cols, int(a["stride"]))
+    return plan
+
+
+def _plan_transpose(a, grid):
+    n_rows, n_cols = int(a["n_rows"]), int(a["n_cols"])
+    _expect_grid("transpose_kernel", grid, (cdiv(n_rows, a["BLOCK_M"]) * cdiv(n_cols, a["BLOCK_N"]),))
+    return "transpose", (Arr("x_ptr"), Arr("out_ptr"), n_rows, n_cols, int(a["stride_x"]), int(a["stride_out"]))
+
+
 REGISTRY = {
     "matmul_kernel": (("a_ptr", "b_ptr", "c_ptr", "M", "N", "K", "stride_am", "stride_ak", "stride_bk",
                        "stride_bn", "stride_cm", "stride_cn", "BLOCK_SIZE_M", "BLOCK_SIZE_N", "BLOCK_SIZE_K",
@@ -175,6 +201,20 @@ REGISTRY = {
                             "BLOCK_SIZE_K", "GROUP_SIZE_M", "ADD_BIAS", "RELU"), _plan_dense),
     "add_kernel": (("x_ptr", "y_ptr", "output_ptr", "n_elements", "BLOCK_SIZE"), _plan_add),
     "layernorm_kernel": (("x_ptr", "out_ptr", "n", "eps", "BLOCK"), _plan_layernorm),
+    "copy_kernel": (("x_ptr", "out_ptr", "n", "BLOCK"), _plan_map("copy", ("x_ptr", "out_ptr"))),
+    "mul_kernel": (("x_ptr", "y_ptr", "out_ptr", "n", "BLOCK"), _plan_map("mul", ("x_ptr", "y_ptr", "out_ptr"))),
+    "fma_kernel": (("x_ptr", "y_ptr", "out_ptr", "n", "alpha", "BLOCK"),
+                   _plan_map("fma", ("x_ptr", "y_ptr", "out_ptr"), (("alpha", float),))),
+    "scaled_relu_kernel": (("x_ptr", "out_ptr", "n", "alpha", "BLOCK"),
+                           _plan_map("scaled_relu", ("x_ptr", "out_ptr"), (("alpha", float),))),
+    "sfu_kernel": (("x_ptr", "out_ptr", "n", "OP", "BLOCK"), _plan_map("sfu", ("x_ptr", "out_ptr"), (("OP", int),))),
+    "log_kernel": (("x_ptr", "out_ptr", "n", "BLOCK"), _plan_map("log", ("x_ptr", "out_ptr"))),
+    "idiv_kernel": (("x_ptr", "y_ptr", "q_ptr", "r_ptr", "n", "BLOCK"),
+                    _plan_map("idiv", ("x_ptr", "y_ptr", "q_ptr", "r_ptr"))),
+    "row_sum_kernel": (("x_ptr", "out_ptr", "n_cols", "stride", "BLOCK_M", "BLOCK_N"), _plan_row_reduce("row_sum")),
+    "row_max_kernel": (("x_ptr", "out_ptr", "n_cols", "stride", "BLOCK_M", "BLOCK_N"), _plan_row_reduce("row_max")),
+    "transpose_kernel": (("x_ptr", "out_ptr", "n_rows", "n_cols", "stride_x", "stride_out", "BLOCK_M", "BLOCK_N"),
+                         _plan_transpose),
 }
 
 

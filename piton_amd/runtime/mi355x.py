@@ -54,6 +54,16 @@ SIGNATURES = {
     "piton_mi355x_linear": [_p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "piton_mi355x_attn_fwd_batched": [_p, _p, _p, _p, _f32] + [_i64] * 16 + [_i32, _i32, _p],
     "piton_mi355x_attn_decode": [_p, _p, _p, _p, _f32] + [_i64] * 13 + [_i32, _p],
+    "piton_mi355x_copy": [_p, _p, _i64, _p],
+    "piton_mi355x_mul": [_p, _p, _p, _i64, _p],
+    "piton_mi355x_fma": [_p, _p, _p, _i64, _f32, _p],
+    "piton_mi355x_scaled_relu": [_p, _p, _i64, _f32, _p],
+    "piton_mi355x_sfu": [_p, _p, _i64, _i32, _p],
+    "piton_mi355x_log": [_p, _p, _i64, _p],
+    "piton_mi355x_idiv": [_p, _p, _p, _p, _i64, _p],
+    "piton_mi355x_row_sum": [_p, _p, _i64, _i64, _i64, _p],
+    "piton_mi355x_row_max": [_p, _p, _i64, _i64, _i64, _p],
+    "piton_mi355x_transpose": [_p, _p, _i64, _i64, _i64, _i64, _p],
 }
 
 
@@ -266,3 +276,71 @@ def attn_decode(q, k, v, out, sm_scale, s_qb, s_qh, s_kb, s_kh, s_kn, s_vb, s_vh
     check_tensor("out", out, max_offset=_span((batch, s_ob), (heads, s_oh), (head_dim, 1)))
     _call("piton_mi355x_attn_decode", _ptr(q), _ptr(k), _ptr(v), _ptr(out), float(sm_scale), s_qb, s_qh, s_kb, s_kh,
           s_kn, s_vb, s_vh, s_vn, s_ob, s_oh, n_keys, batch, heads, int(head_dim), _stream())
+
+
+# ---- the perf suite's primitives (perf/suite.py:323-351) -----------------------------------
+
+def _elementwise(entry, n, tensors, *scalars):
+    for name, t in tensors:
+        check_tensor(name, t, max_offset=n - 1)
+    _call(entry, *[_ptr(t) for _, t in tensors], n, *scalars, _stream())
+
+
+def copy(x, out, n):
+    """copy_kernel (examples/primitive_kernels.py:12-17)."""
+    _elementwise("piton_mi355x_copy", n, (("x", x), ("out", out)))
+
+
+def mul(x, y, out, n):
+    """mul_kernel (examples/elementwise.py:5-9)."""
+    _elementwise("piton_mi355x_mul", n, (("x", x), ("y", y), ("out", out)))
+
+
+def fma(x, y, out, n, alpha):
+    """fma_kernel (examples/primitive_kernels.py:20-27): out = x * alpha + y."""
+    _elementwise("piton_mi355x_fma", n, (("x", x), ("y", y), ("out", out)), float(alpha))
+
+
+def scaled_relu(x, out, n, alpha):
+    """scaled_relu_kernel (examples/kernels.py:79-85)."""
+    _elementwise("piton_mi355x_scaled_relu", n, (("x", x), ("out", out)), float(alpha))
+
+
+def sfu(x, out, n, op):
+    """sfu_kernel (examples/sfu_tests.py:5-22): OP 0 exp2, 1 log2, 2 1/x, 3 1/sqrt, 4 exp, 5 sqrt."""
+    _elementwise("piton_mi355x_sfu", n, (("x", x), ("out", out)), int(op))
+
+
+def log(x, out, n):
+    """log_kernel (examples/primitive_kernels.py:70-76)."""
+    _elementwise("piton_mi355x_log", n, (("x", x), ("out", out)))
+
+
+def idiv(x, y, q, r, n):
+    """idiv_kernel (examples/primitive_kernels.py:30-38): C-style int32 quotient and remainder."""
+    for name, t in (("x", x), ("y", y), ("q", q), ("r", r)):
+        check_tensor(name, t, dtype=torch.int32, max_offset=n - 1)
+    _call("piton_mi355x_idiv", _ptr(x), _ptr(y), _ptr(q), _ptr(r), n, _stream())
+
+
+def _row_reduce(entry, x, out, rows, n_cols, stride):
+    check_tensor("x", x, max_offset=_span((rows, stride), (n_cols, 1)))
+    check_tensor("out", out, max_offset=rows - 1)
+    _call(entry, _ptr(x), _ptr(out), rows, n_cols, stride, _stream())
+
+
+def row_sum(x, out, rows, n_cols, stride):
+    """row_sum_kernel (examples/kernels.py:88-96)."""
+    _row_reduce("piton_mi355x_row_sum", x, out, rows, n_cols, stride)
+
+
+def row_max(x, out, rows, n_cols, stride):
+    """row_max_kernel (examples/primitive_kernels.py:41-50)."""
+    _row_reduce("piton_mi355x_row_max", x, out, rows, n_cols, stride)
+
+
+def transpose(x, out, n_rows, n_cols, stride_x, stride_out):
+    """transpose_kernel (examples/primitive_kernels.py:53-67): out[c, r] = x[r, c]."""
+    check_tensor("x", x, max_offset=_span((n_rows, stride_x), (n_cols, 1)))
+    check_tensor("out", out, max_offset=_span((n_cols, stride_out), (n_rows, 1)))
+    _call("piton_mi355x_transpose", _ptr(x), _ptr(out), n_rows, n_cols, stride_x, stride_out, _stream())

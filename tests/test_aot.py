@@ -33,9 +33,17 @@ SPECS = {
                            "RELU=True"),
     "add_kernel": ("x_ptr=*fp32,y_ptr=*fp32,output_ptr=*fp32,n_elements=i32", "BLOCK_SIZE=1024"),
     "layernorm_kernel": ("x_ptr=*fp32,out_ptr=*fp32,n=i32,eps=fp32", "BLOCK=256"),
+    "fma_kernel": ("x_ptr=*fp32,y_ptr=*fp32,out_ptr=*fp32,n=i32,alpha=fp32", "BLOCK=256"),
+    "sfu_kernel": ("x_ptr=*fp32,out_ptr=*fp32,n=i32", "OP=4,BLOCK=256"),
+    "idiv_kernel": ("x_ptr=*i32,y_ptr=*i32,q_ptr=*i32,r_ptr=*i32,n=i32", "BLOCK=256"),
+    "row_sum_kernel": ("x_ptr=*fp32,out_ptr=*fp32,n_cols=i32,stride=i32", "BLOCK_M=4,BLOCK_N=64"),
+    "transpose_kernel": ("x_ptr=*fp32,out_ptr=*fp32,n_rows=i32,n_cols=i32,stride_x=i32,stride_out=i32",
+                         "BLOCK_M=16,BLOCK_N=16"),
 }
 KERNEL_FILES = {"matmul_kernel": "tutorial.py", "softmax_kernel": "tutorial.py", "add_kernel": "tutorial.py",
-                "layernorm_kernel": "tutorial.py", "attn_fwd_kernel": "attention.py", "dense_layer_kernel": "nn.py"}
+                "layernorm_kernel": "tutorial.py", "attn_fwd_kernel": "attention.py", "dense_layer_kernel": "nn.py",
+                "fma_kernel": "primitives.py", "sfu_kernel": "primitives.py", "idiv_kernel": "primitives.py",
+                "row_sum_kernel": "primitives.py", "transpose_kernel": "primitives.py"}
 
 
 def generate(tmp, kernel, name):

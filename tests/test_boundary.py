@@ -151,11 +151,11 @@ def test_plans_check_grids_before_the_device():
 
 def test_unknown_kernels_are_refused():
     @piton_amd.jit
-    def scaled_relu_kernel(x_ptr, out_ptr, n, alpha, BLOCK: tl.constexpr):
+    def mandelbrot_kernel(out_ptr, x0, y0, step, width, max_iter, BLOCK: tl.constexpr):
         pass
 
     with pytest.raises(NotImplementedError):
-        scaled_relu_kernel[(1,)](np.zeros(4, np.float32), np.zeros(4, np.float32), 4, 0.5, BLOCK=4)
+        mandelbrot_kernel[(1,)](np.zeros(4, np.int32), -0.5, 0.0, 0.01, 4, 10, BLOCK=4)
 
     @piton_amd.jit
     def matmul_kernel(a_ptr, b_ptr, c_ptr, M, N, K):  # same name, other parameters

@@ -69,15 +69,27 @@ static int launch_map(const float *x, const float *y, float *out, int64_t n, flo
     return check_launch(what);
 }
 
-// C-style (truncating) quotient and remainder: q = trunc(x / y), r = x - q y
+// C-style (truncating) quotient and remainder: q = trunc(x / y), r = x - q y. VEC: four
+// elements per thread through 16-byte vectors (i indexes vectors), else one.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void idiv_kernel(const int32_t *x, const int32_t *y, int32_t *q, int32_t *r,
-                                                   int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+                                                   int64_t begin, int64_t n) {
+    const int64_t i = begin + (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const int32_t a = x[i], b = y[i];
-    const int32_t qq = a / b;
-    q[i] = qq;
-    r[i] = a - qq * b;
+    if constexpr (VEC) {
+        const i32x4 a = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(x) + i);
+        const i32x4 b = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(y) + i);
+        const i32x4 qq = a / b;
+        __builtin_nontemporal_store(qq, reinterpret_cast<i32x4 *>(q) + i);
+        __builtin_nontemporal_store(a - qq * b, reinterpret_cast<i32x4 *>(r) + i);
+    } else {
+        const int32_t a = x[i], b = y[i];
+        const int32_t qq = a / b;
+        q[i] = qq;
+        r[i] = a - qq * b;
+    }
 }
 
 // out[r] = sum / max of x[r, 0:n_cols] (row stride `stride`), one wave per row
@@ -193,8 +205,15 @@ int32_t piton_mi355x_idiv(const int32_t *x, const int32_t *y, int32_t *q, int32_
     int rc = require_device();
     if (rc) return rc;
     if (n == 0) return PITON_OK;
-    hipLaunchKernelGGL(idiv_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, y, q, r,
-                       n);
+    hipStream_t st = (hipStream_t)stream;
+    const bool vec = aligned16(x) && aligned16(y) && aligned16(q) && aligned16(r);
+    const int64_t n4 = vec ? n / 4 : 0;
+    if (n4 > 0)
+        hipLaunchKernelGGL(idiv_kernel<true>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, x, y, q, r,
+                           (int64_t)0, n4);
+    if (4 * n4 < n)
+        hipLaunchKernelGGL(idiv_kernel<false>, dim3((unsigned)((n - 4 * n4 + 255) / 256)), dim3(256), 0, st, x, y,
+                           q, r, 4 * n4, n);
     return finish(check_launch("idiv"));
 }
 

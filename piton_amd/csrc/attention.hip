@@ -356,111 +356,255 @@ __device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
-// The fast kernel: head_dim == D, Q / K / V rows contiguous and 16-byte aligned (K in [N, D]
-// order), every row offset of a head within 2^31 bytes (checked on the host). Same blocks and
-// arithmetic as the general kernel, but Q, K and V come through buffer descriptors bounded at
-// the head's last row: a lane's addresses are 32-bit byte offsets that advance by one constant
-// per block, rows past n_ctx read as zeros, and nothing is guarded.
-template <int D>
-__global__ __launch_bounds__(64 * ANW) __attribute__((amdgpu_waves_per_eu(PITON_ATTN_WAVES_PER_EU)))
-void attn_fwd_fast(AttnArgs g) {
-    __shared__ float vslab[ANW][ABN][D];
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, half = lane >> 5, l31 = lane & 31;
-    int64_t bh;
-    int qg;
-    map_group(g, bh, qg);
-    const int64_t bi = bh / g.n_heads, h = bh % g.n_heads;
-    const int q0 = qg * AQG, qi = q0 + l31, n_ctx = (int)g.n_ctx;
-    const uint32_t s_qm = (uint32_t)g.s_qm, s_kn = (uint32_t)g.s_kn, s_vn = (uint32_t)g.s_vn;
+// The fast kernel: head_dim == D, Q / K / V / O rows contiguous and 16-byte aligned (K in
+// [N, D] order), every row offset of a head within 2^31 bytes (checked on the host). Per query
+// group it runs the general kernel's blocks and arithmetic (wave w takes key blocks w, w + ANW,
+// ..., the same online softmax and the same merge formula), so the two agree bit for bit:
+//   * Q, K and V come through buffer descriptors bounded at the head's last row. Loads past it
+//     return zeros, LDS-DMA loads included, so nothing is guarded and every block, the partial
+//     last one too, takes one code path (which also keeps the compiler's memory waits exact);
+//   * Q' (pre-scaled) lives in LDS transposed (qT[d][query]): the score product's B operand is
+//     a conflict-free LDS read instead of 32 registers per lane;
+//   * V blocks are copied from memory straight into the wave's LDS slab (16-byte LDS-DMA);
+//   * software pipeline: block j+1's score product is issued beside block j's exps, K is loaded
+//     two blocks ahead and V one block ahead; the first block's K and V are requested before
+//     Q is staged, so those latencies overlap;
+//   * PAIR (causal): the workgroup runs query group nqg-1-p, then group p, so each workgroup
+//     visits nqg + 1 key blocks. A wave parks its first group's state in registers and the
+//     pipeline runs on into the second group without a barrier; both merge at the end;
+//   * the merge is spread over the four waves, each finishing a quarter of every output row.
+#ifndef PITON_ATTN_FAST_WAVES
+#define PITON_ATTN_FAST_WAVES 3
+#endif
+// causal query groups in pairs: 0 never, 1 always, 2 when the pairs fill at most two
+// workgroups per CU (one generation)
+#ifndef PITON_ATTN_PAIR_MODE
+#define PITON_ATTN_PAIR_MODE 2
+#endif
 
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+template <int D>
+__device__ __forceinline__ f32x16 block_scores_lds(const float (&kf)[D / 2], const float (*qT)[AQG], int half,
+                                                   int l31) {
+    f32x16 st;
+#pragma unroll
+    for (int r = 0; r < 16; r++) st[r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < D / 2; s++)
+        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qT[half * (D / 2) + s][l31], st, 0, 0, 0);
+    return st;
+}
+
+// Causal pairs: workgroup -> (batch*head, pair rank p), whole heads per XCD as in map_group.
+__device__ __forceinline__ void map_pair(const AttnArgs &g, int64_t &bh, int &prank) {
+    const int npair = (g.nqg + 1) / 2, nbh = g.nbh;
+    if (nbh % kXcdCount == 0) {
+        const int xcd = blockIdx.x % kXcdCount, i = blockIdx.x / kXcdCount, per = nbh / kXcdCount;
+        bh = (int64_t)xcd * per + i % per;
+        prank = i / per;
+    } else {
+        bh = blockIdx.x / npair;
+        prank = blockIdx.x % npair;
+    }
+}
+
+// One query group's merge from the ANW wave states in LDS (xo[w][slot][lane] with slot
+// b*16 + r for o[b][r], xm[w][0|1][lane] = m, l): merge_store's arithmetic (wave 0's state
+// first, then waves 1.. in order), wave w finishing slots [w*D/8, (w+1)*D/8) of every lane,
+// four consecutive dims per float4 store.
+template <int D>
+__device__ __forceinline__ void merge_quarter(const float (*xo)[D / 2][64], const float (*xm)[2][64], float *op,
+                                              bool row_ok) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5;
+    float m = xm[0][0][lane];
+#pragma unroll
+    for (int w = 1; w < ANW; w++) m = fmaxf(m, xm[w][0][lane]);
+    const float mu = m == -INFINITY ? 0.f : m;
+    const float c0 = __builtin_amdgcn_exp2f(xm[0][0][lane] - mu);
+    float cw[ANW - 1];
+    float l = xm[0][1][lane] * c0;
+#pragma unroll
+    for (int w = 1; w < ANW; w++) {
+        cw[w - 1] = __builtin_amdgcn_exp2f(xm[w][0][lane] - mu);
+        l += xm[w][1][lane] * cw[w - 1];
+    }
+    const float inv = 1.0f / l;
+    if (!row_ok) return;
+    constexpr int SPW = D / 2 / ANW;
+#pragma unroll
+    for (int i = 0; i < SPW; i += 4) {
+        const int s0 = wave * SPW + i, b = s0 >> 4, r = s0 & 15;
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float acc = xo[0][s0 + e][lane] * c0;
+#pragma unroll
+            for (int w = 1; w < ANW; w++) acc += xo[w][s0 + e][lane] * cw[w - 1];
+            v[e] = acc * inv;
+        }
+        *reinterpret_cast<f32x4 *>(op + b * 32 + 8 * (r >> 2) + 4 * half) = v;
+    }
+}
+
+template <int D, bool PAIR>
+__global__ __launch_bounds__(64 * ANW) __attribute__((amdgpu_waves_per_eu(PAIR ? 2 : PITON_ATTN_FAST_WAVES)))
+void attn_fwd_fast(AttnArgs g) {
+    constexpr int NG = PAIR ? 2 : 1;
+    constexpr int SLAB_F = ANW * ABN * D, COMPUTE_F = SLAB_F + NG * D * AQG;
+    constexpr int STATE_F = ANW * (D / 2 + 2) * 64, MERGE_F = NG * STATE_F;  // every wave's (O, m, l) per group
+    __shared__ __attribute__((aligned(16))) float lds[COMPUTE_F > MERGE_F ? COMPUTE_F : MERGE_F];
+    float(*vslab)[ABN][D] = reinterpret_cast<float(*)[ABN][D]>(lds);
+    float(*qT)[D][AQG] = reinterpret_cast<float(*)[D][AQG]>(lds + SLAB_F);
+
+    const int t = threadIdx.x, lane = t & 63, half = lane >> 5, l31 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    int64_t bh;
+    int qg0, qg1 = 0, ng = 1;
+    if constexpr (PAIR) {
+        int p;
+        map_pair(g, bh, p);
+        qg0 = g.nqg - 1 - p;
+        qg1 = p;
+        ng = p != qg0 ? 2 : 1;
+    } else {
+        map_group(g, bh, qg0);
+    }
+    const int64_t bi = bh / g.n_heads, h = bh % g.n_heads;
+    const int n_ctx = (int)g.n_ctx;
+    const uint32_t s_qm = (uint32_t)g.s_qm, s_kn = (uint32_t)g.s_kn, s_vn = (uint32_t)g.s_vn;
     const auto rq = make_rsrc(g.q + bi * g.s_qb + h * g.s_qh, ((uint32_t)(n_ctx - 1) * s_qm + D) * 4u);
     const auto rk = make_rsrc(g.k + bi * g.s_kb + h * g.s_kh, ((uint32_t)(n_ctx - 1) * s_kn + D) * 4u);
     const auto rv = make_rsrc(g.v + bi * g.s_vb + h * g.s_vh, ((uint32_t)(n_ctx - 1) * s_vn + D) * 4u);
 
-    float qf[D / 2];
-    {
-        const uint32_t off = ((uint32_t)qi * s_qm + half * (D / 2)) * 4u;
-#pragma unroll
-        for (int c = 0; c < D / 8; c++) {
-            const f32x4 f = bload4(rq, off + 16u * c);
-#pragma unroll
-            for (int j = 0; j < 4; j++) qf[4 * c + j] = f[j] * g.scale;
-        }
-    }
-    f32x16 o[D / 32];
-#pragma unroll
-    for (int b = 0; b < D / 32; b++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) o[b][r] = 0.f;
-    float m_i = -INFINITY, l_i = 0.f;
-
+    // this wave's blocks: list index j < n0 is block wave + ANW*j of the first group, j >= n0
+    // block wave + ANW*(j - n0) of the second (the heavier group comes first, so n0 >= n1)
     const int nkb_all = (n_ctx + ABN - 1) / ABN;
-    const int nkb = g.causal ? min(nkb_all, qg + 1) : nkb_all;
+    const int nkb0 = g.causal ? min(nkb_all, qg0 + 1) : nkb_all, nkb1 = min(nkb_all, qg1 + 1);
+    const int n0 = nkb0 > wave ? (nkb0 - wave + ANW - 1) / ANW : 0;
+    const int n1 = (PAIR && ng > 1 && nkb1 > wave) ? (nkb1 - wave + ANW - 1) / ANW : 0;
+    const int n = n0 + n1;
+    auto kb_of = [&](int j) { return wave + ANW * (j < n0 ? j : j - n0); };
 
-    // byte offsets: K half row of key kb*32 + l31; V chunk c of the block at v_off + c * v_c
+    // byte offsets: K half row of key kb*32 + l31; V chunk c of block kb at v_lane + kb*v_blk + c*v_c
     constexpr int KPC = 64 / (D / 4);  // V keys per float4 chunk step of the lane
     constexpr int NVQ = ABN * D / 4 / 64;
-    uint32_t k_off = ((uint32_t)(wave * ABN + l31) * s_kn + half * (D / 2)) * 4u;
-    uint32_t v_off = ((uint32_t)(wave * ABN + lane / (D / 4)) * s_vn + 4 * (lane % (D / 4))) * 4u;
-    const uint32_t k_step = (uint32_t)(ANW * ABN) * s_kn * 4u, v_step = (uint32_t)(ANW * ABN) * s_vn * 4u;
-    const uint32_t v_c = (uint32_t)KPC * s_vn * 4u;
-
-    float(*vw)[D] = reinterpret_cast<float(*)[D]>(&vslab[wave][0][0]);
-    auto load_k = [&](float (&kf)[D / 2]) {
+    const uint32_t k_lane = ((uint32_t)l31 * s_kn + half * (D / 2)) * 4u, k_blk = (uint32_t)ABN * s_kn * 4u;
+    const uint32_t v_lane = ((uint32_t)(lane / (D / 4)) * s_vn + 4 * (lane % (D / 4))) * 4u;
+    const uint32_t v_blk = (uint32_t)ABN * s_vn * 4u, v_c = (uint32_t)KPC * s_vn * 4u;
+    float(*vw)[D] = vslab[wave];
+    auto load_k = [&](float (&kf)[D / 2], int kb) {
+        const uint32_t off = k_lane + (uint32_t)kb * k_blk;
 #pragma unroll
         for (int c = 0; c < D / 8; c++) {
-            const f32x4 f = bload4(rk, k_off + 16u * c);
+            const f32x4 f = bload4(rk, off + 16u * c);
 #pragma unroll
             for (int j = 0; j < 4; j++) kf[4 * c + j] = f[j];
         }
-        k_off += k_step;
     };
-    auto load_v = [&](f32x4 (&vr)[NVQ]) {
+    // V of block kb into the slab by LDS-DMA: lane l's 16 bytes of chunk c land at row
+    // KPC*c + l / (D/4), dims 4*(l % (D/4)) (the slab's row-major layout); rows past n_ctx
+    // arrive as zeros
+    auto fetch_v = [&](int kb) {
+        const uint32_t off = v_lane + (uint32_t)kb * v_blk;
 #pragma unroll
-        for (int c = 0; c < NVQ; c++) vr[c] = bload4(rv, v_off + v_c * c);
-        v_off += v_step;
+        for (int c = 0; c < NVQ; c++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)&vw[KPC * c][0], 16, off + v_c * c, 0, 0, 0);
     };
 
-    // Software pipeline over this wave's blocks kb = wave, wave + ANW, ...: while block kb's
-    // exps run on the vector unit, block kb + ANW's score product runs on the matrix cores;
-    // each load is issued as soon as its registers are free (K right after the product that
-    // reads it, V right after it is staged), a whole block ahead of its use. Loads of a block
-    // past the last one read zeros or unused rows (never out of the buffers) and are dropped.
-    int kb = wave;
-    if (kb < nkb) {
-        float kf[D / 2];
-        f32x4 vr[NVQ];
-        load_k(kf);
-        f32x16 st = block_scores<D>(kf, qf);
-        // the loop starts with the next block's K issued before this block's V, the order it
-        // keeps every iteration, so each wait on K lets the newer V loads stay in flight
-        load_k(kf);
-        __builtin_amdgcn_sched_barrier(0);  // keep that order through instruction scheduling
-        load_v(vr);
-        auto step = [&](auto has_next) {
+    float kf[D / 2];
+    if (n > 0) {  // the first block's K and V are in flight while Q is staged
+        load_k(kf, kb_of(0));
+        fetch_v(kb_of(0));
+    }
+    // Q'^T of the groups: qT[gi][d][j] = Q[qg_gi*AQG + j][d] * sm_scale * log2 e (rows past n_ctx: 0)
+    for (int i = t; i < NG * AQG * D / 4; i += 64 * ANW) {
+        const int gi = i / (AQG * D / 4), r = i % (AQG * D / 4), j = r / (D / 4), dq = r % (D / 4);
+        const f32x4 f = bload4(rq, ((uint32_t)((gi ? qg1 : qg0) * AQG + j) * s_qm + 4 * dq) * 4u);
+#pragma unroll
+        for (int e = 0; e < 4; e++) qT[gi][4 * dq + e][j] = f[e] * g.scale;
+    }
+    __syncthreads();
+
+    f32x16 o[D / 32], po[D / 32];  // the running state and (PAIR) the parked first group's
+#pragma unroll
+    for (int b = 0; b < D / 32; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[b][r] = po[b][r] = 0.f;
+    float m_i = -INFINITY, l_i = 0.f, pm = -INFINITY, pl = 0.f;
+
+    if (n > 0) {
+        f32x16 st = block_scores_lds<D>(kf, qT[0], half, l31);
+        // the loop starts with the next block's K issued before this block's V is waited for,
+        // the order it keeps every iteration, so each wait on K lets newer V loads stay in flight
+        load_k(kf, kb_of(1));  // past the list it reads a block nobody uses (or zeros)
+        __builtin_amdgcn_sched_barrier(0);
+        auto step = [&](int j, auto has_next) {
             constexpr bool NEXT = decltype(has_next)::value;
-            mask_scores(st, kb * ABN, n_ctx, g.causal, q0, qi, half);
+            const int q0 = (PAIR && j >= n0 ? qg1 : qg0) * AQG;
+            mask_scores(st, kb_of(j) * ABN, n_ctx, g.causal, q0, q0 + l31, half);
             const float mref = online_rescale<D>(st, m_i, l_i, o);
             f32x16 st_next;
-            if constexpr (NEXT) st_next = block_scores<D>(kf, qf);
+            if constexpr (NEXT) st_next = block_scores_lds<D>(kf, qT[PAIR && j + 1 >= n0 ? 1 : 0], half, l31);
             online_exp(st, mref, l_i);
-            if constexpr (NEXT) load_k(kf);
-            wave_lds_sync();  // the previous block's operand reads are done with the slab
-#pragma unroll
-            for (int c = 0; c < NVQ; c++) {
-                const int idx = lane + 64 * c;
-                *reinterpret_cast<f32x4 *>(&vw[idx / (D / 4)][4 * (idx % (D / 4))]) = vr[c];
-            }
-            wave_lds_sync();  // rows staged by other lanes are visible to the operand reads
-            if constexpr (NEXT) load_v(vr);
+            if constexpr (NEXT) load_k(kf, kb_of(j + 2));
+            // block j's V is in the slab once at most the 8 K loads just issued are in flight
+            // (vmcnt counts in issue order; the scheduling barriers keep that order)
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(NEXT ? 0x0F78 : 0x0F70);  // vmcnt(8) / vmcnt(0)
+            __builtin_amdgcn_sched_barrier(0);
+            wave_lds_sync();  // rows written for other lanes are visible to the operand reads
             block_pv<D>(o, st, vw, half, l31);
-            if constexpr (NEXT) st = st_next;
+            if constexpr (NEXT) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the operand reads have their data
+                __builtin_amdgcn_sched_barrier(0);
+                wave_lds_sync();
+                fetch_v(kb_of(j + 1));
+                st = st_next;
+                if (PAIR && j + 1 == n0) {  // the next block opens the second group
+#pragma unroll
+                    for (int b = 0; b < D / 32; b++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            po[b][r] = o[b][r];
+                            o[b][r] = 0.f;
+                        }
+                    pm = m_i;
+                    pl = l_i;
+                    m_i = -INFINITY;
+                    l_i = 0.f;
+                }
+            }
         };
-        for (; kb + ANW < nkb; kb += ANW) step(std::true_type{});
-        step(std::false_type{});
+        int j = 0;
+        for (; j + 1 < n; j++) step(j, std::true_type{});
+        step(j, std::false_type{});
     }
-    merge_store<D>(&vslab[0][0][0], o, m_i, l_i, g.o + bi * g.s_ob + h * g.s_oh + (int64_t)qi * g.s_om, qi < n_ctx,
-                   D);
+
+    // merge: every wave's state of every group into LDS, then each wave a quarter of the rows
+    float(*xs)[STATE_F] = reinterpret_cast<float(*)[STATE_F]>(lds);
+    auto put = [&](int gi, const f32x16 (&so)[D / 32], float sm, float sl) {
+        float(*xo)[D / 2][64] = reinterpret_cast<float(*)[D / 2][64]>(xs[gi]);
+        float(*xm)[2][64] = reinterpret_cast<float(*)[2][64]>(xs[gi] + ANW * (D / 2) * 64);
+#pragma unroll
+        for (int b = 0; b < D / 32; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) xo[wave][b * 16 + r][lane] = so[b][r];
+        xm[wave][0][lane] = sm;
+        xm[wave][1][lane] = sl;
+    };
+    __syncthreads();  // every wave is done with its slab and the Q tiles
+    const bool second = PAIR && n1 > 0;  // the running state is the second group's
+    put(second ? 1 : 0, o, m_i, l_i);
+    if (PAIR && ng > 1) put(second ? 0 : 1, po, pm, pl);
+    __syncthreads();
+    for (int gi = 0; gi < ng; gi++) {
+        const int qi = (gi ? qg1 : qg0) * AQG + l31;
+        merge_quarter<D>(reinterpret_cast<const float(*)[D / 2][64]>(xs[gi]),
+                         reinterpret_cast<const float(*)[2][64]>(xs[gi] + ANW * (D / 2) * 64),
+                         g.o + bi * g.s_ob + h * g.s_oh + (int64_t)qi * g.s_om, qi < n_ctx);
+    }
 }
 
 template <int D>
@@ -571,16 +715,28 @@ static int attn_launch(AttnArgs g, int64_t batch, int64_t n_heads, int32_t head_
                     head_dim % 4 == 0) ? K_VEC_D : K_SCALAR;
     g.nqg = (int)((g.n_ctx + AQG - 1) / AQG);
     g.nbh = (int)(batch * n_heads);
-    const dim3 grid((unsigned)((int64_t)g.nqg * g.nbh));
+    dim3 grid((unsigned)((int64_t)g.nqg * g.nbh));
     // the fast kernel: exact head_dim, contiguous aligned rows that do not overlap, and every
     // byte offset it forms (rows up to n_ctx + 3 * ANW * 32, the loads a few blocks past the
     // end included) within 31 bits
     const int64_t smax = std::max(g.s_qm, std::max(g.s_kn, g.s_vn));
     const bool fast = (head_dim == 32 || head_dim == 64) && kl == K_VEC_D && g.q_vec && g.v_vec &&
+                      aligned16(g.o) && g.s_om % 4 == 0 && g.s_oh % 4 == 0 && g.s_ob % 4 == 0 &&
                       g.s_qm >= head_dim && g.s_kn >= head_dim && g.s_vn >= head_dim &&
                       ((g.n_ctx + 3 * ANW * ABN + AQG) * smax + head_dim) * 4 < (1LL << 31);
-    if (fast && head_dim == 64) hipLaunchKernelGGL(attn_fwd_fast<64>, grid, dim3(64 * ANW), 0, st, g);
-    else if (fast) hipLaunchKernelGGL(attn_fwd_fast<32>, grid, dim3(64 * ANW), 0, st, g);
+    bool pair = false;
+    if (fast && g.causal && g.nqg > 1) {
+        const int64_t pairs = (int64_t)g.nbh * ((g.nqg + 1) / 2);
+        pair = PITON_ATTN_PAIR_MODE == 1 || (PITON_ATTN_PAIR_MODE == 2 && pairs <= 2 * (int64_t)device_cu_count());
+        if (pair) grid = dim3((unsigned)pairs);
+    }
+    if (fast && head_dim == 64) {
+        if (pair) hipLaunchKernelGGL((attn_fwd_fast<64, true>), grid, dim3(64 * ANW), 0, st, g);
+        else hipLaunchKernelGGL((attn_fwd_fast<64, false>), grid, dim3(64 * ANW), 0, st, g);
+    } else if (fast) {
+        if (pair) hipLaunchKernelGGL((attn_fwd_fast<32, true>), grid, dim3(64 * ANW), 0, st, g);
+        else hipLaunchKernelGGL((attn_fwd_fast<32, false>), grid, dim3(64 * ANW), 0, st, g);
+    }
     else if (head_dim <= 32) launch_d<32>(kl, g, grid, st);
     else if (head_dim == 64) launch_d<64>(kl, g, grid, st);
     else launch_d<128>(kl, g, grid, st);

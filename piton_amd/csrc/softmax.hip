@@ -9,7 +9,9 @@
 //     each wave and then through LDS across the four. Many short-lived workgroups keep reads
 //     and writes interleaved across the chip; at 4096 x 4096 this streams ~8 % faster than
 //     a single generation of row-per-wave waves, which read together and then write together;
-//   * loads and stores are nontemporal: the row is touched once;
+//   * stores are nontemporal (the output is not read back here); the workgroup-per-row
+//     kernel loads through the ordinary cached path, which streams ~13 % faster there than
+//     nontemporal loads, the wave-per-row kernel nontemporally (~8 % faster there);
 //   * rows need not be 16-byte aligned (n = 1823): each row is read through the aligned
 //     float4 window that covers it, and elements outside [0, n) of the row are masked to
 //     -inf. An aligned 16-byte block lies inside one page, so the window never touches an
@@ -35,6 +37,14 @@
 #ifndef PITON_SM_LONG
 #define PITON_SM_LONG 2
 #endif
+// chunks per thread of the workgroup kernel: mid class 2 (256 threads) or 1 (512); long
+// class 4 (256 threads) or 2 (512)
+#ifndef PITON_SM_MID_CH
+#define PITON_SM_MID_CH 2
+#endif
+#ifndef PITON_SM_LONG_CH
+#define PITON_SM_LONG_CH 2
+#endif
 
 namespace piton {
 
@@ -50,7 +60,7 @@ __device__ __forceinline__ float exp_row(float d) {
 // Loads row r's aligned float4 window into b: T threads share the row, thread t holding
 // chunks t, t + T, ... (CH of them); elements of the window outside the row are masked when
 // the row is processed.
-template <int CH, int T, bool ALIGNED>
+template <int CH, int T, bool ALIGNED, bool NT>
 __device__ __forceinline__ void load_row(const float *in, int64_t in_rs, int64_t r, int n, int lane,
                                          f32x4 (&b)[CH], int &off) {
     const float *rp = in + r * in_rs;
@@ -61,14 +71,14 @@ __device__ __forceinline__ void load_row(const float *in, int64_t in_rs, int64_t
     for (int c = 0; c < CH; c++) {
         const int ci = lane + T * c;
         f32x4 f = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        if (ci < nch) f = __builtin_nontemporal_load(src + ci);
+        if (ci < nch) f = NT ? __builtin_nontemporal_load(src + ci) : src[ci];
         b[c] = f;
     }
 }
 
-// Reduction over the T threads that share a row: one wavefront by DPP lane moves; four by
-// DPP, then the four wave results through LDS (slot picks a separate LDS pair per use, so
-// one barrier per reduction suffices; the sum adds the waves in a fixed order).
+// Reduction over the T threads that share a row: one wavefront by DPP lane moves; T/64 of
+// them by DPP, then the wave results through LDS (each use has its own T/64 LDS slots, so one
+// barrier per reduction suffices; the waves combine in a fixed pairwise order).
 template <int T, class Op>
 __device__ __forceinline__ float row_reduce(float v, Op op, float *red) {
     v = wave_reduce(v, op);
@@ -76,11 +86,12 @@ __device__ __forceinline__ float row_reduce(float v, Op op, float *red) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (lane == 0) red[wave] = v;
     __syncthreads();
-    return op(op(red[0], red[1]), op(red[2], red[3]));
+    if (T == 256) return op(op(red[0], red[1]), op(red[2], red[3]));
+    return op(op(op(red[0], red[1]), op(red[2], red[3])), op(op(red[4], red[5]), op(red[6], red[7])));
 }
 
 // Masks row `row` (held in b, window offset off) to [0, n), normalises it and stores it.
-// lane: this thread's index among the T threads of the row; red: 8 floats of LDS when T = 256.
+// lane: this thread's index among the T threads of the row; red: 2 * T / 64 floats of LDS.
 template <int CH, int T, bool ALIGNED>
 __device__ __forceinline__ void softmax_store_row(float *out, int64_t out_rs, int64_t row, int n, int lane,
                                                   f32x4 (&b)[CH], int off, float *red) {
@@ -117,7 +128,7 @@ __device__ __forceinline__ void softmax_store_row(float *out, int64_t out_rs, in
             s += e;
         }
     }
-    s = row_reduce<T>(s, SumOp(), red + 4);
+    s = row_reduce<T>(s, SumOp(), red + T / 64);
     const float inv = 1.0f / s;
 
     float *op = out + row * out_rs;
@@ -169,30 +180,30 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float *out, const flo
 
     f32x4 a[CH], b[CH];
     int off_a, off_b = 0;
-    load_row<CH, 64, ALIGNED>(in, in_rs, row, n, lane, a, off_a);
+    load_row<CH, 64, ALIGNED, true>(in, in_rs, row, n, lane, a, off_a);
     while (true) {
-        if (row + W < rows) load_row<CH, 64, ALIGNED>(in, in_rs, row + W, n, lane, b, off_b);
+        if (row + W < rows) load_row<CH, 64, ALIGNED, true>(in, in_rs, row + W, n, lane, b, off_b);
         softmax_store_row<CH, 64, ALIGNED>(out, out_rs, row, n, lane, a, off_a, nullptr);
         row += W;
         if (row >= rows) break;
-        if (row + W < rows) load_row<CH, 64, ALIGNED>(in, in_rs, row + W, n, lane, a, off_a);
+        if (row + W < rows) load_row<CH, 64, ALIGNED, true>(in, in_rs, row + W, n, lane, a, off_a);
         softmax_store_row<CH, 64, ALIGNED>(out, out_rs, row, n, lane, b, off_b, nullptr);
         row += W;
         if (row >= rows) break;
     }
 }
 
-// One 256-thread workgroup per row (rows of 1025..16384 window chunks, CH chunks per
-// thread): many short-lived workgroups keep the chip's reads and writes interleaved, which
-// streams faster than a single generation of row-per-wave waves.
-template <int CH, bool ALIGNED>
-__global__ __launch_bounds__(256) void softmax_wg_kernel(float *out, const float *in, int64_t in_rs, int64_t out_rs,
-                                                         int n) {
-    __shared__ float red[8];
+// One T-thread workgroup per row (T = 256 or 512, CH chunks per thread): many short-lived
+// workgroups keep the chip's reads and writes interleaved, which streams faster than a single
+// generation of row-per-wave waves.
+template <int CH, int T, bool ALIGNED>
+__global__ __launch_bounds__(T) void softmax_wg_kernel(float *out, const float *in, int64_t in_rs, int64_t out_rs,
+                                                       int n) {
+    __shared__ float red[2 * T / 64];
     f32x4 b[CH];
     int off;
-    load_row<CH, 256, ALIGNED>(in, in_rs, blockIdx.x, n, threadIdx.x, b, off);
-    softmax_store_row<CH, 256, ALIGNED>(out, out_rs, blockIdx.x, n, threadIdx.x, b, off, red);
+    load_row<CH, T, ALIGNED, false>(in, in_rs, blockIdx.x, n, threadIdx.x, b, off);
+    softmax_store_row<CH, T, ALIGNED>(out, out_rs, blockIdx.x, n, threadIdx.x, b, off, red);
 }
 
 // Rows too long for registers: one workgroup per row, three passes over the row.
@@ -283,13 +294,13 @@ extern "C" int32_t piton_mi355x_softmax(float *out, const float *in, int64_t in_
         else                                                                                                        \
             launch_rows<CH, false>(mode, wgs, st, out, in, in_row_stride, out_row_stride, (int)n, n_rows);         \
     } while (0)
-#define PITON_SM_WG(CH)                                                                                             \
+#define PITON_SM_WG(CH, T)                                                                                          \
     do {                                                                                                            \
         if (aligned)                                                                                                \
-            hipLaunchKernelGGL((softmax_wg_kernel<CH, true>), dim3((unsigned)n_rows), block, 0, st, out, in,        \
+            hipLaunchKernelGGL((softmax_wg_kernel<CH, T, true>), dim3((unsigned)n_rows), dim3(T), 0, st, out, in,   \
                                in_row_stride, out_row_stride, (int)n);                                              \
         else                                                                                                        \
-            hipLaunchKernelGGL((softmax_wg_kernel<CH, false>), dim3((unsigned)n_rows), block, 0, st, out, in,       \
+            hipLaunchKernelGGL((softmax_wg_kernel<CH, T, false>), dim3((unsigned)n_rows), dim3(T), 0, st, out, in,  \
                                in_row_stride, out_row_stride, (int)n);                                              \
     } while (0)
     PITON_REQUIRE(mode != 2 || n_rows <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "softmax: too many rows");
@@ -298,11 +309,11 @@ extern "C" int32_t piton_mi355x_softmax(float *out, const float *in, int64_t in_
     else if (per_lane <= 2) PITON_SM(2);
     else if (per_lane <= 4) PITON_SM(4);
     else if (per_lane <= 8 && mode != 2) PITON_SM(8);
-    else if (per_lane <= 8) PITON_SM_WG(2);
+    else if (per_lane <= 8) PITON_SM_WG(PITON_SM_MID_CH, PITON_SM_MID_CH == 2 ? 256 : 512);
     else if (per_lane <= 16 && mode != 2) PITON_SM(16);
-    else if (per_lane <= 16) PITON_SM_WG(4);
-    else if (per_lane <= 32) PITON_SM_WG(8);
-    else if (per_lane <= 64) PITON_SM_WG(16);
+    else if (per_lane <= 16) PITON_SM_WG(PITON_SM_LONG_CH, 64 * PITON_SM_LONG_CH == 256 ? 256 : 512);
+    else if (per_lane <= 32) PITON_SM_WG(8, 256);
+    else if (per_lane <= 64) PITON_SM_WG(16, 256);
     else
         hipLaunchKernelGGL(softmax_long_kernel, dim3((unsigned)n_rows), block, 0, st, out, in, in_row_stride,
                            out_row_stride, n);

@@ -135,14 +135,15 @@ def bench_matmul(n, steps, warmup):
 
 
 def bench_softmax(n, rows=4096, launches=48):
-    """Cold-cache GB/s: buffer pairs rotated over > 512 MB so each launch reads from HBM; the
-    launches replay from a HIP graph, back to back."""
+    """Cold-cache GB/s: buffer pairs rotated so the inputs span >= 1 GiB, four times the
+    256 MB last-level cache, and each launch reads from HBM; the launches replay from a HIP
+    graph, back to back."""
     import torch
 
     from piton_amd import next_power_of_2
     from piton_amd.runtime import mi355x as rt
     pair_bytes = 2 * 4 * rows * n
-    pairs = max(2, -(-512 * 2 ** 20 // pair_bytes))
+    pairs = max(2, -(-2 ** 30 // (pair_bytes // 2)))
     g = torch.Generator(device="cuda").manual_seed(n)
     xs = [torch.randn((rows, n), device="cuda", generator=g) * 4 for _ in range(pairs)]
     ys = [torch.empty_like(x) for x in xs]

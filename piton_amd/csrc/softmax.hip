@@ -9,9 +9,8 @@
 //     each wave and then through LDS across the four. Many short-lived workgroups keep reads
 //     and writes interleaved across the chip; at 4096 x 4096 this streams ~8 % faster than
 //     a single generation of row-per-wave waves, which read together and then write together;
-//   * stores are nontemporal (the output is not read back here); the workgroup-per-row
-//     kernel loads through the ordinary cached path, which streams ~13 % faster there than
-//     nontemporal loads, the wave-per-row kernel nontemporally (~8 % faster there);
+//   * loads and stores are nontemporal: the row is touched once. (Cached loads look faster
+//     only while the inputs fit the 256 MB last-level cache; from HBM they are ~3 % slower);
 //   * rows need not be 16-byte aligned (n = 1823): each row is read through the aligned
 //     float4 window that covers it, and elements outside [0, n) of the row are masked to
 //     -inf. An aligned 16-byte block lies inside one page, so the window never touches an
@@ -60,7 +59,7 @@ __device__ __forceinline__ float exp_row(float d) {
 // Loads row r's aligned float4 window into b: T threads share the row, thread t holding
 // chunks t, t + T, ... (CH of them); elements of the window outside the row are masked when
 // the row is processed.
-template <int CH, int T, bool ALIGNED, bool NT>
+template <int CH, int T, bool ALIGNED>
 __device__ __forceinline__ void load_row(const float *in, int64_t in_rs, int64_t r, int n, int lane,
                                          f32x4 (&b)[CH], int &off) {
     const float *rp = in + r * in_rs;
@@ -71,7 +70,7 @@ __device__ __forceinline__ void load_row(const float *in, int64_t in_rs, int64_t
     for (int c = 0; c < CH; c++) {
         const int ci = lane + T * c;
         f32x4 f = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        if (ci < nch) f = NT ? __builtin_nontemporal_load(src + ci) : src[ci];
+        if (ci < nch) f = __builtin_nontemporal_load(src + ci);
         b[c] = f;
     }
 }
@@ -180,13 +179,13 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float *out, const flo
 
     f32x4 a[CH], b[CH];
     int off_a, off_b = 0;
-    load_row<CH, 64, ALIGNED, true>(in, in_rs, row, n, lane, a, off_a);
+    load_row<CH, 64, ALIGNED>(in, in_rs, row, n, lane, a, off_a);
     while (true) {
-        if (row + W < rows) load_row<CH, 64, ALIGNED, true>(in, in_rs, row + W, n, lane, b, off_b);
+        if (row + W < rows) load_row<CH, 64, ALIGNED>(in, in_rs, row + W, n, lane, b, off_b);
         softmax_store_row<CH, 64, ALIGNED>(out, out_rs, row, n, lane, a, off_a, nullptr);
         row += W;
         if (row >= rows) break;
-        if (row + W < rows) load_row<CH, 64, ALIGNED, true>(in, in_rs, row + W, n, lane, a, off_a);
+        if (row + W < rows) load_row<CH, 64, ALIGNED>(in, in_rs, row + W, n, lane, a, off_a);
         softmax_store_row<CH, 64, ALIGNED>(out, out_rs, row, n, lane, b, off_b, nullptr);
         row += W;
         if (row >= rows) break;
@@ -202,7 +201,7 @@ __global__ __launch_bounds__(T) void softmax_wg_kernel(float *out, const float *
     __shared__ float red[2 * T / 64];
     f32x4 b[CH];
     int off;
-    load_row<CH, T, ALIGNED, false>(in, in_rs, blockIdx.x, n, threadIdx.x, b, off);
+    load_row<CH, T, ALIGNED>(in, in_rs, blockIdx.x, n, threadIdx.x, b, off);
     softmax_store_row<CH, T, ALIGNED>(out, out_rs, blockIdx.x, n, threadIdx.x, b, off, red);
 }
 

@@ -120,6 +120,26 @@ def test_numpy_arrays_copy_in_copy_out():
     np.testing.assert_array_equal(b, b0)
 
 
+@pytest.mark.parametrize("M,N,K,pad", [(256, 384, 96, (4, 8, 3)), (128, 128, 32, (0, 0, 0)), (384, 128, 2080, (8, 4, 1))])
+def test_whole_tile_shapes_with_padded_rows(M, N, K, pad):
+    """Shapes whose tiles are all whole (M, N multiples of 128, K of 32) take the unguarded
+    kernel: padded row strides of A, B and C must not leak into the product or past C's rows."""
+    rng = np.random.default_rng(M + N + K)
+    a = dyadic(rng, (M, K))
+    b = dyadic(rng, (K, N))
+    A = torch.zeros((M, K + pad[0]), device="cuda")
+    B = torch.zeros((K, N + pad[1]), device="cuda")
+    C = torch.full((M, N + pad[2]), -7.0, device="cuda")
+    A[:, :K] = torch.from_numpy(a).cuda()
+    A[:, K:] = float("nan")
+    B[:, :N] = torch.from_numpy(b).cuda()
+    B[:, N:] = float("nan")
+    run(A[:, :K], B[:, :N], C[:, :N])
+    got = C.cpu().numpy()
+    np.testing.assert_array_equal(got[:, :N], a @ b)
+    assert (got[:, N:] == -7.0).all()
+
+
 @pytest.mark.parametrize("group", [1, 3, 8, 64])
 def test_group_order_does_not_change_bits(group):
     g = torch.Generator(device="cuda").manual_seed(11)

@@ -119,7 +119,8 @@ def test_row_reduction_reads_whole_chunks_like_the_reference():
     within(out, x[:, :128].astype(np.float64).sum(axis=1), 1e-5, 1e-5)
 
 
-@pytest.mark.parametrize("rows,cols,pad", [(MAT, MAT, 0), (100, 37, 3), (1, 300, 0), (513, 64, 1)])
+@pytest.mark.parametrize("rows,cols,pad", [(MAT, MAT, 0), (100, 37, 3), (1, 300, 0), (513, 64, 1),
+                                           (260, 132, 4), (64, 8, 0), (4, 4100, 8), (1028, 196, 12)])
 def test_transpose_exact(rows, cols, pad):
     g = Inputs()
     x = np.zeros((rows, cols + pad), np.float32)

@@ -51,6 +51,22 @@ def test_config_shape_causal_1024():
     assert fp64.rel_fro(out[:1], ref[:1]) <= fp64.rel_fro(emu, ref[:1])
 
 
+@pytest.mark.parametrize("heads,n,d", [(40, 1056, 64), (72, 1000, 32), (24, 2080, 64)])
+def test_many_causal_groups_take_the_single_group_grid(heads, n, d):
+    """Causal launches with more query-group pairs than two per CU run one group per
+    workgroup (three waves per SIMD) instead of pairs; ragged N leaves a partial last block.
+    Same tolerance as the config shape, and the pairing must not change any bits: a prefix of
+    the heads (few enough to be paired) gives the same output for those heads."""
+    q, k, v = qkv(n, d, seed=heads + n, heads=heads)
+    tq, tk, tv = (torch.from_numpy(t).cuda() for t in (q, k, v))
+    out = run_attention(tq, tk, tv, causal=True).cpu().numpy()
+    ref = fp64.attention_reference(q, k, v, True)
+    assert fp64.rel_fro(out, ref) <= TOL
+    np.testing.assert_allclose(out, ref, rtol=0, atol=2e-5)
+    few = run_attention(tq[:2].contiguous(), tk[:2].contiguous(), tv[:2].contiguous(), causal=True).cpu().numpy()
+    np.testing.assert_array_equal(few, out[:2])
+
+
 def test_single_key_returns_v():
     q, k, v = qkv(1, 64, seed=9)
     out = run_attention(q, k, v, causal=False)

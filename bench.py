@@ -6,7 +6,8 @@ plus the row softmax (HBM GB/s, cold cache) and causal attention at their benchm
 Prints ONE JSON line. A "step" is one matmul_kernel launch over A, B (4096 x 4096, U[-1, 1],
 already resident in HBM). `value` is 2*M*N*K*steps / the timed region's wall time. The
 `roofline` object is the matmul kernel's: algorithmic FLOPs per launch / its average launch
-time (HIP events on the launch stream) against the 157.3 TFLOP/s dense fp32 MFMA peak. The
+time (HIP events on the launch stream at the two ends of the timed region, / steps) against
+the 157.3 TFLOP/s dense fp32 MFMA peak. The
 `cpu_baseline` object is the oracle (the C restatement of the reference's round-toward-zero
 emulator arithmetic) timed on a bounded sample of rows of the same product on this host.
 """
@@ -89,18 +90,6 @@ def pmc_probe(n):
     torch.cuda.synchronize()
 
 
-def timed(fn, iters, stream):
-    """Per-launch durations (s) from HIP events recorded on the launch stream."""
-    import torch
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
-    for i, (s, e) in enumerate(evs):
-        s.record(stream)
-        fn(i)
-        e.record(stream)
-    torch.cuda.synchronize()
-    return [s.elapsed_time(e) * 1e-3 for s, e in evs]
-
-
 def timed_graph(fn, iters, reps=5):
     from piton_amd.timing import timed_graph as tg
     return tg(fn, iters, reps)
@@ -134,12 +123,19 @@ def bench_matmul(n, steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    # timed region: K steps bracketed by synchronize on both sides
+    # timed region: K steps bracketed by synchronize on both sides; HIP events on the launch
+    # stream at its two ends give the average launch duration (no events between launches,
+    # which would put a marker packet between every two kernels)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    durs = timed(step, steps, stream)
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     flops = 2.0 * n * n * n
-    return dict(wall=wall, durs=durs, flops=flops, a=a, b=b, c=c)
+    return dict(wall=wall, kernel_s=e0.elapsed_time(e1) * 1e-3 / steps, flops=flops, a=a, b=b, c=c)
 
 
 def bench_softmax(n, rows=4096, launches=48):
@@ -270,7 +266,7 @@ def main():
         pmc_probe(n)
         return
     mm = bench_matmul(n, args.steps, args.warmup)
-    avg = sum(mm["durs"]) / len(mm["durs"])
+    avg = mm["kernel_s"]
     achieved = mm["flops"] / avg
     value = mm["flops"] * args.steps / mm["wall"] / 1e12
     line = {

@@ -337,57 +337,48 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int64_
 
 // Y = X W (+ bias, ReLU, + residual) for at most 64 rows (a decode step's batch): the big
 // kernel would give such a product a handful of 128 x 128 tiles walking K serially. Here a
-// workgroup owns all the rows and 16 columns (v_mfma_f32_16x16x4f32, four 16-row tiles); its
-// 16 waves split K, and each lane group of 16 lanes takes a contiguous quarter of its wave's K
-// range (the MFMA's 4-deep k index is permuted that way), so a lane walks consecutive k. With
-// K a multiple of 256 and 16-byte X rows, a lane loads X as float4 (four k at once) and the
-// loads of the next four k are in flight while the current four multiply. The 16 partial
-// tiles sum in a fixed order through LDS: results do not depend on timing.
+// workgroup owns one 16-row tile and 16 columns (v_mfma_f32_16x16x4f32; the grid is column
+// blocks x row tiles, so a 64 x 256 product spreads over 64 CUs: with all four row tiles in
+// one workgroup the product was MFMA-bound on 16 CUs, 2.4 us per 256 of K); its 16 waves
+// split K, and each lane group of 16 lanes takes a contiguous quarter of its wave's K range
+// (the MFMA's 4-deep k index is permuted that way), so a lane walks consecutive k. With K a
+// multiple of 256 and 16-byte X rows, a lane loads X as float4 (four k at once) and the loads
+// of the next four k are in flight while the current four multiply. The 16 partial tiles sum
+// in a fixed order through LDS: results do not depend on timing.
 constexpr int SMN = 16;        // columns per workgroup
 constexpr int SMWAVES = 16;    // waves splitting K
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 template <bool FAST>
 __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) {
-    __shared__ float part[SMWAVES][4][4][64];  // [wave][row tile][accumulator][lane]: 64 KiB
+    __shared__ float part[SMWAVES][4][64];  // [wave][accumulator][lane]: 16 KiB
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 4, c16 = lane & 15;
     const int64_t n0 = (int64_t)blockIdx.x * SMN, n = n0 + c16;
+    const int64_t m0 = (int64_t)blockIdx.y * 16;  // this workgroup's 16-row tile
     const int64_t kq = (g.K + 4 * SMWAVES - 1) / (4 * SMWAVES);  // k per lane group
     const int64_t kbeg = (int64_t)(wave * 4 + grp) * kq;
     const bool n_ok = n < g.N;
-    f32x4v acc[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    const int64_t m = m0 + c16;  // the A row this lane supplies
+    const bool m_ok = m < g.M;
+    f32x4v acc = f32x4v{0.f, 0.f, 0.f, 0.f};
     if constexpr (FAST) {
         // kq % 4 == 0 and every k of the range < K; rows past M and columns past N read zeros
         const float *wp = g.b + (n_ok ? n : 0) + kbeg * g.s_bk;
-        const float *xp[4];
-        bool m_ok[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int64_t m = 16 * i + c16;
-            m_ok[i] = m < g.M;
-            xp[i] = g.a + (m_ok[i] ? m : 0) * g.s_am + kbeg;
-        }
-        auto load = [&](int64_t s, f32x4v (&xa)[4], float (&wb)[4]) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const f32x4v v = *reinterpret_cast<const f32x4v *>(xp[i] + s);
-                xa[i] = m_ok[i] ? v : f32x4v{0.f, 0.f, 0.f, 0.f};
-            }
+        const float *xp = g.a + (m_ok ? m : 0) * g.s_am + kbeg;
+        auto load = [&](int64_t s, f32x4v &xa, float (&wb)[4]) {
+            const f32x4v v = *reinterpret_cast<const f32x4v *>(xp + s);
+            xa = m_ok ? v : f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float v = wp[(s + j) * g.s_bk];
-                wb[j] = n_ok ? v : 0.f;
+                const float w = wp[(s + j) * g.s_bk];
+                wb[j] = n_ok ? w : 0.f;
             }
         };
-        auto mul = [&](const f32x4v (&xa)[4], const float (&wb)[4]) {
+        auto mul = [&](const f32x4v &xa, const float (&wb)[4]) {
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[i][j], wb[j], acc[i], 0, 0, 0);
+            for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], wb[j], acc, 0, 0, 0);
         };
-        f32x4v xa0[4], xa1[4];
+        f32x4v xa0, xa1;
         float wb0[4], wb1[4];
         load(0, xa0, wb0);
         for (int64_t s = 0; s < kq; s += 8) {
@@ -403,31 +394,26 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
             const int64_t k = kbeg + s;
             const bool k_ok = k < g.K;
             const float bv = (k_ok && n_ok) ? wp[k * g.s_bk] : 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int64_t m = 16 * i + c16;
-                const float av = (k_ok && m < g.M) ? g.a[m * g.s_am + k] : 0.f;
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i], 0, 0, 0);
-            }
+            const float av = (k_ok && m_ok) ? g.a[m * g.s_am + k] : 0.f;
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
         }
     }
-    // accumulator r of row tile i holds row 16*i + 4*grp + r, column n0 + c16
+    // accumulator r holds row m0 + 4*grp + r, column n0 + c16
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) part[wave][i][r][lane] = acc[i][r];
+    for (int r = 0; r < 4; r++) part[wave][r][lane] = acc[r];
     __syncthreads();
-    // thread (i, r, lane) = (t / 256, t / 64 % 4, t % 64) finishes one output
-    const int i = t >> 8, r = (t >> 6) & 3;
-    const int64_t m = 16 * i + 4 * grp + r;
-    if (m >= g.M || !n_ok) return;
-    float v = part[0][i][r][lane];
+    if (t >= 256) return;
+    // thread (r, lane) = (t / 64, t % 64) finishes one output: the 16 partials in wave order
+    const int r = t >> 6;
+    const int64_t mo = m0 + 4 * grp + r;
+    if (mo >= g.M || !n_ok) return;
+    float v = part[0][r][lane];
 #pragma unroll
-    for (int w = 1; w < SMWAVES; w++) v += part[w][i][r][lane];
+    for (int w = 1; w < SMWAVES; w++) v += part[w][r][lane];
     if (g.bias) v += g.bias[n];
     if (g.relu && v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
-    if (g.res) v += g.res[m * g.s_rm + n];
-    g.c[m * g.s_cm + n] = v;
+    if (g.res) v += g.res[mo * g.s_rm + n];
+    g.c[mo * g.s_cm + n] = v;
 }
 
 static int layout_a(const GemmArgs &g) {
@@ -533,7 +519,7 @@ int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *w, const f
     GemmArgs g{x, w, y, M, N, K, ldx, 1, N, 1, ldy, 1, 1, bias, relu ? 1 : 0, residual, ldr, 0, 0};
     if (M > 0 && M <= 64) {
         PITON_REQUIRE((N + SMN - 1) / SMN <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "linear: N=%lld too large", (long long)N);
-        const dim3 grid((unsigned)((N + SMN - 1) / SMN)), block(64 * SMWAVES);
+        const dim3 grid((unsigned)((N + SMN - 1) / SMN), (unsigned)((M + 15) / 16)), block(64 * SMWAVES);
         if (K % (16 * SMWAVES) == 0 && ldx % 4 == 0 && aligned16(x))
             hipLaunchKernelGGL(gemm_small_m_kernel<true>, grid, block, 0, (hipStream_t)stream, g);
         else

@@ -130,6 +130,17 @@ PITON_API int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *
                             const float *residual, int64_t ldr, float *y, int64_t ldy, int64_t M,
                             int64_t N, int64_t K, int32_t relu, void *stream);
 
+/* piton_mi355x_linear of layer-normalised rows: Y = LN(X) W (+ bias) (ReLU) (+ R), where
+ * LN(x) = (x - mean) / sqrt(var + eps) over each row's K columns with the statistics of
+ * piton_mi355x_layernorm (the layernorm_kernel of tests/test_reroll_reduce.py:199-208), so the
+ * result equals layernorm followed by linear bit for bit. No reference counterpart: it serves
+ * the decoder's per-token steps (one launch instead of two). Needs M <= 64, K % 256 == 0 and
+ * 16-byte-aligned X rows; anything else returns PITON_EUNSUPPORTED. */
+PITON_API int32_t piton_mi355x_linear_ln(const float *x, int64_t ldx, float eps, const float *w,
+                               const float *bias, const float *residual, int64_t ldr, float *y,
+                               int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t relu,
+                               void *stream);
+
 /* attn_fwd_kernel (examples/attention.py:67-113) over batch x n_heads heads: grid row y is
  * head y % n_heads of batch y / n_heads, whose Q / K / V / Out start at b*stride_?b + h*stride_?h.
  * piton_mi355x_attn_fwd is the batch = 1 case. */

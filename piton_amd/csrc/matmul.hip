@@ -42,6 +42,7 @@ struct GemmArgs {
     const float *res;   // residual added after bias / ReLU (nullable), element (m, n) at m*s_rm + n
     int64_t s_rm;
     int a_kfast, b_nfast;  // scalar loaders: which index runs fastest across threads
+    float ln_eps;          // small-row kernel with LN: rows of A are layer-normalised first
 };
 
 // Loads the A tile (GBM x GBK at m0, k0) into 16 registers per thread.
@@ -349,9 +350,16 @@ constexpr int SMN = 16;        // columns per workgroup
 constexpr int SMWAVES = 16;    // waves splitting K
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-template <bool FAST>
+// LN: Y = LN(X) W (...), LN(x) = (x - mean) * (1 / sqrt(var + eps)) over the K columns of each
+// row with the statistics computed exactly as layernorm_rows_kernel computes them for a
+// 16-byte-aligned row (per lane (x0 + x1) + (x2 + x3) over its float4 chunks, DPP wave sums,
+// a second pass of fmaf squares): the product sees the very values the separate layernorm
+// would have written. Needs the FAST layout.
+template <bool FAST, bool LN>
 __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) {
+    static_assert(!LN || FAST, "LN needs the FAST layout");
     __shared__ float part[SMWAVES][4][64];  // [wave][accumulator][lane]: 16 KiB
+    __shared__ float stats[16][2];          // LN: mean and 1/sqrt(var + eps) of the tile's rows
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, grp = lane >> 4, c16 = lane & 15;
     const int64_t n0 = (int64_t)blockIdx.x * SMN, n = n0 + c16;
     const int64_t m0 = (int64_t)blockIdx.y * 16;  // this workgroup's 16-row tile
@@ -361,12 +369,50 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
     const int64_t m = m0 + c16;  // the A row this lane supplies
     const bool m_ok = m < g.M;
     f32x4v acc = f32x4v{0.f, 0.f, 0.f, 0.f};
+    float ln_mean = 0.f, ln_inv = 1.f;
+    if constexpr (LN) {
+        // wave w: the statistics of row m0 + w (K % 256 == 0, so a lane's chunks are lane + 64c)
+        const int64_t mr = m0 + wave;
+        if (mr < g.M) {
+            const f32x4v *src = reinterpret_cast<const f32x4v *>(g.a + mr * g.s_am);
+            const int64_t nch = g.K / 4;
+            float sum = 0.f;
+            for (int64_t ci = lane; ci < nch; ci += 64) {
+                const f32x4v f = src[ci];
+                sum += (f[0] + f[1]) + (f[2] + f[3]);
+            }
+            const float mean = wave_reduce(sum, SumOp()) / (float)g.K;
+            float q = 0.f;
+            for (int64_t ci = lane; ci < nch; ci += 64) {
+                const f32x4v f = src[ci];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float d = f[j] - mean;
+                    q = fmaf(d, d, q);
+                }
+            }
+            const float var = wave_reduce(q, SumOp()) / (float)g.K;
+            if (lane == 0) {
+                stats[wave][0] = mean;
+                stats[wave][1] = 1.0f / sqrtf(var + g.ln_eps);
+            }
+        }
+        __syncthreads();
+        if (m_ok) {
+            ln_mean = stats[c16][0];
+            ln_inv = stats[c16][1];
+        }
+    }
     if constexpr (FAST) {
         // kq % 4 == 0 and every k of the range < K; rows past M and columns past N read zeros
         const float *wp = g.b + (n_ok ? n : 0) + kbeg * g.s_bk;
         const float *xp = g.a + (m_ok ? m : 0) * g.s_am + kbeg;
         auto load = [&](int64_t s, f32x4v &xa, float (&wb)[4]) {
-            const f32x4v v = *reinterpret_cast<const f32x4v *>(xp + s);
+            f32x4v v = *reinterpret_cast<const f32x4v *>(xp + s);
+            if constexpr (LN) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[j] = (v[j] - ln_mean) * ln_inv;
+            }
             xa = m_ok ? v : f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -516,18 +562,45 @@ int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *w, const f
                   "linear: pointers must be 4-byte aligned");
     int rc = require_device();
     if (rc) return rc;
-    GemmArgs g{x, w, y, M, N, K, ldx, 1, N, 1, ldy, 1, 1, bias, relu ? 1 : 0, residual, ldr, 0, 0};
+    GemmArgs g{x, w, y, M, N, K, ldx, 1, N, 1, ldy, 1, 1, bias, relu ? 1 : 0, residual, ldr, 0, 0, 0.f};
     if (M > 0 && M <= 64) {
         PITON_REQUIRE((N + SMN - 1) / SMN <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "linear: N=%lld too large", (long long)N);
         const dim3 grid((unsigned)((N + SMN - 1) / SMN), (unsigned)((M + 15) / 16)), block(64 * SMWAVES);
         if (K % (16 * SMWAVES) == 0 && ldx % 4 == 0 && aligned16(x))
-            hipLaunchKernelGGL(gemm_small_m_kernel<true>, grid, block, 0, (hipStream_t)stream, g);
+            hipLaunchKernelGGL((gemm_small_m_kernel<true, false>), grid, block, 0, (hipStream_t)stream, g);
         else
-            hipLaunchKernelGGL(gemm_small_m_kernel<false>, grid, block, 0, (hipStream_t)stream, g);
+            hipLaunchKernelGGL((gemm_small_m_kernel<false, false>), grid, block, 0, (hipStream_t)stream, g);
         rc = check_launch("linear");
     } else {
         rc = launch_gemm(g, (hipStream_t)stream, "linear");
     }
+    if (rc == PITON_OK) clear_error();
+    return rc;
+}
+
+int32_t piton_mi355x_linear_ln(const float *x, int64_t ldx, float eps, const float *w, const float *bias,
+                               const float *residual, int64_t ldr, float *y, int64_t ldy, int64_t M, int64_t N,
+                               int64_t K, int32_t relu, void *stream) {
+    using namespace piton;
+    PITON_REQUIRE(M >= 0 && N > 0 && K > 0, PITON_EINVAL, "linear_ln: bad size M=%lld N=%lld K=%lld", (long long)M,
+                  (long long)N, (long long)K);
+    PITON_REQUIRE(ldx >= K && ldy >= N && (!residual || ldr >= N), PITON_EINVAL,
+                  "linear_ln: row strides (%lld, %lld, %lld) shorter than the rows", (long long)ldx, (long long)ldy,
+                  (long long)ldr);
+    PITON_REQUIRE(M == 0 || (x && w && y), PITON_EINVAL, "linear_ln: null X, W or Y");
+    PITON_REQUIRE(aligned4(x) && aligned4(w) && aligned4(y) && aligned4(bias) && aligned4(residual), PITON_EINVAL,
+                  "linear_ln: pointers must be 4-byte aligned");
+    PITON_REQUIRE(M <= 64 && K % (16 * SMWAVES) == 0 && ldx % 4 == 0 && aligned16(x), PITON_EUNSUPPORTED,
+                  "linear_ln: needs M <= 64, K %% 256 == 0 and 16-byte X rows (M=%lld K=%lld ldx=%lld)",
+                  (long long)M, (long long)K, (long long)ldx);
+    PITON_REQUIRE((N + SMN - 1) / SMN <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "linear_ln: N=%lld too large", (long long)N);
+    int rc = require_device();
+    if (rc) return rc;
+    if (M == 0) return PITON_OK;
+    GemmArgs g{x, w, y, M, N, K, ldx, 1, N, 1, ldy, 1, 1, bias, relu ? 1 : 0, residual, ldr, 0, 0, eps};
+    const dim3 grid((unsigned)((N + SMN - 1) / SMN), (unsigned)((M + 15) / 16)), block(64 * SMWAVES);
+    hipLaunchKernelGGL((gemm_small_m_kernel<true, true>), grid, block, 0, (hipStream_t)stream, g);
+    rc = check_launch("linear_ln");
     if (rc == PITON_OK) clear_error();
     return rc;
 }

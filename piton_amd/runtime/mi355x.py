@@ -52,6 +52,7 @@ SIGNATURES = {
     "piton_mi355x_argmax_rows": [_p, _i64, _i64, _i64, _p, _p],
     "piton_mi355x_embedding": [_p, _i64, _i64, _p, _p, _p] + [_i64] * 7 + [_p, _p],
     "piton_mi355x_linear": [_p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p],
+    "piton_mi355x_linear_ln": [_p, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "piton_mi355x_attn_fwd_batched": [_p, _p, _p, _p, _f32] + [_i64] * 16 + [_i32, _i32, _p],
     "piton_mi355x_attn_decode": [_p, _p, _p, _p, _f32] + [_i64] * 13 + [_i32, _p],
     "piton_mi355x_copy": [_p, _p, _i64, _p],
@@ -253,6 +254,18 @@ def linear(x, ldx, w, bias, residual, ldr, y, ldy, M, N, K, relu=False):
     check_tensor("y", y, max_offset=_span((M, ldy), (N, 1)))
     _call("piton_mi355x_linear", _ptr(x), ldx, _ptr(w), _ptr(bias), _ptr(residual), ldr, _ptr(y), ldy, M, N, K,
           int(bool(relu)), _stream())
+
+
+def linear_ln(x, ldx, eps, w, bias, residual, ldr, y, ldy, M, N, K, relu=False):
+    """Y = [ReLU](LN(X) W [+ b]) [+ R]: layernorm then linear in one launch, bit-identical to the
+    two (M <= 64, K % 256 == 0, 16-byte X rows; else MI355XError with status -2)."""
+    check_tensor("x", x, max_offset=_span((M, ldx), (K, 1)))
+    check_tensor("w", w, max_offset=K * N - 1)
+    check_tensor("bias", bias, max_offset=N - 1, allow_none=True)
+    check_tensor("residual", residual, max_offset=_span((M, ldr), (N, 1)), allow_none=True)
+    check_tensor("y", y, max_offset=_span((M, ldy), (N, 1)))
+    _call("piton_mi355x_linear_ln", _ptr(x), ldx, float(eps), _ptr(w), _ptr(bias), _ptr(residual), ldr, _ptr(y), ldy,
+          M, N, K, int(bool(relu)), _stream())
 
 
 def attn_fwd_batched(q, k, v, out, sm_scale, s_qb, s_qh, s_qm, s_kb, s_kh, s_kn, s_kk, s_vb, s_vh, s_vn, s_ob, s_oh,

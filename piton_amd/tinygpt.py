@@ -101,12 +101,18 @@ class TinyGPT:
         rt.embedding(self.tokens[r0:], 1, B, self.w["tok"], self.w["pos"][p0:], x, D, B * D, B, p1 - p0, D, V, 0,
                      self.err)
         scale = 1.0 / float(np.sqrt(Dh))
+        # a decode step's products have at most 64 rows: layernorm fuses into the next linear
+        # (the same values bit for bit, one launch instead of two)
+        fuse_ln = n <= 64 and D % 256 == 0
         for i in range(cfg.n_layers):
             w = lambda k: self.w[f"{k}{i}"]  # noqa: E731
             cache = self.qkv[i]
             qkv = cache[r0:r0 + n]
-            rt.layernorm(x, h, D, cfg.eps, n, D)
-            rt.linear(h, D, w("wqkv"), w("bqkv"), None, 0, qkv, 3 * D, n, 3 * D, D)
+            if fuse_ln:
+                rt.linear_ln(x, D, cfg.eps, w("wqkv"), w("bqkv"), None, 0, qkv, 3 * D, n, 3 * D, D)
+            else:
+                rt.layernorm(x, h, D, cfg.eps, n, D)
+                rt.linear(h, D, w("wqkv"), w("bqkv"), None, 0, qkv, 3 * D, n, 3 * D, D)
             if p0 == 0:
                 # prefix: batched causal flash attention over positions [0, p1)
                 rt.attn_fwd_batched(cache, cache[:, D:], cache[:, 2 * D:], self.att, scale,
@@ -118,12 +124,18 @@ class TinyGPT:
                 rt.attn_decode(qkv, cache[:, D:], cache[:, 2 * D:], att, scale, 3 * D, Dh, 3 * D, Dh,
                                B * 3 * D, 3 * D, Dh, B * 3 * D, D, Dh, p1, B, H, Dh)
             rt.linear(att, D, w("wo"), w("bo"), x, D, x, D, n, D, D)
-            rt.layernorm(x, h, D, cfg.eps, n, D)
-            rt.linear(h, D, w("w1"), w("b1"), None, 0, mlp, F, n, F, D, relu=True)
+            if fuse_ln:
+                rt.linear_ln(x, D, cfg.eps, w("w1"), w("b1"), None, 0, mlp, F, n, F, D, relu=True)
+            else:
+                rt.layernorm(x, h, D, cfg.eps, n, D)
+                rt.linear(h, D, w("w1"), w("b1"), None, 0, mlp, F, n, F, D, relu=True)
             rt.linear(mlp, F, w("w2"), w("b2"), x, D, x, D, n, D, F)
         last = (p1 - 1) * B
-        rt.layernorm(self.x[last:last + B], self.h[last:last + B], D, cfg.eps, B, D)
-        rt.linear(self.h[last:last + B], D, self.w["lm"], None, None, 0, self.logits, V, B, V, D)
+        if B <= 64 and D % 256 == 0:
+            rt.linear_ln(self.x[last:last + B], D, cfg.eps, self.w["lm"], None, None, 0, self.logits, V, B, V, D)
+        else:
+            rt.layernorm(self.x[last:last + B], self.h[last:last + B], D, cfg.eps, B, D)
+            rt.linear(self.h[last:last + B], D, self.w["lm"], None, None, 0, self.logits, V, B, V, D)
         rt.argmax_rows(self.logits, B, V, V, self.tokens[p1 * B:(p1 + 1) * B])
 
     def _decode(self, T0: int, steps: int, kv_cache: bool):

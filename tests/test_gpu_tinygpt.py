@@ -66,6 +66,44 @@ def test_linear_up_to_64_rows(M, N, K, relu):
     np.testing.assert_array_equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("M,N,K,relu,ldx", [(64, 768, 256, False, 256), (64, 1024, 256, True, 260),
+                                            (64, 256, 256, False, 256), (17, 100, 512, True, 516),
+                                            (1, 16, 256, False, 256)])
+def test_layernorm_fused_linear_equals_the_two_launches(M, N, K, relu, ldx):
+    """linear_ln = layernorm then linear, bit for bit (the decoder's decode steps fuse them),
+    with bias, ReLU, a residual and strided rows; and within 1e-6 of float64."""
+    rng = np.random.default_rng(M + N + K)
+    x = (rng.standard_normal((M, ldx)) * 3 + 1).astype(np.float32)
+    w = rng.standard_normal((K, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    r = rng.standard_normal((M, N)).astype(np.float32)
+    tx, tw, tb, tr = (torch.from_numpy(t).cuda() for t in (x, w, b, r))
+    eps = 1e-5
+    h = torch.empty((M, ldx), device="cuda")  # the layernorm entry writes with the input's row stride
+    rt.layernorm(tx, h, K, eps, M, ldx)
+    two = torch.full((M, N), -2.0, device="cuda")
+    rt.linear(h, ldx, tw, tb, tr, N, two, N, M, N, K, relu=relu)
+    one = torch.full((M, N), -3.0, device="cuda")
+    rt.linear_ln(tx, ldx, eps, tw, tb, tr, N, one, N, M, N, K, relu=relu)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(one.cpu().numpy(), two.cpu().numpy())
+    xd = x[:, :K].astype(np.float64)
+    hd = (xd - xd.mean(1, keepdims=True)) / np.sqrt(xd.var(1, keepdims=True) + eps)
+    pre = hd @ w + b
+    ref = (np.maximum(pre, 0) if relu else pre) + r
+    assert fp64.rel_fro(one.cpu().numpy(), ref) <= 1e-6
+
+
+def test_layernorm_fused_linear_refuses_unsupported_shapes():
+    x = torch.zeros((65, 256), device="cuda")
+    w = torch.zeros((256, 16), device="cuda")
+    y = torch.zeros((65, 16), device="cuda")
+    with pytest.raises(rt.MI355XError):
+        rt.linear_ln(x, 256, 1e-5, w, None, None, 0, y, 16, 65, 16, 256)  # more than 64 rows
+    with pytest.raises(rt.MI355XError):
+        rt.linear_ln(x, 256, 1e-5, w[:200], None, None, 0, y, 16, 64, 16, 200)  # K % 256 != 0
+
+
 def test_position_major_attention_prefill_and_decode():
     """The decoder's layout: qkv rows t*B + b of 3*D; heads through strides."""
     rng = np.random.default_rng(1)

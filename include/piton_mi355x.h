@@ -130,6 +130,18 @@ PITON_API int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *
                             const float *residual, int64_t ldr, float *y, int64_t ldy, int64_t M,
                             int64_t N, int64_t K, int32_t relu, void *stream);
 
+/* The digits MLP chain (examples/digits_model.py:120-139: three dense_layer_kernel launches of
+ * examples/nn_kernels.py:23-74 with ReLU on the hidden layers, then numpy's argmax of the
+ * first n_classes logits) in one launch: x [M, k0] row-major, w_l [K_l, N_l] row-major, biases
+ * nullable. logits [M, n3] (nullable) are bit-identical to the three piton_mi355x_dense launches;
+ * pred (nullable) gets the predictions. Layer sizes even and <= 256 (n3 <= 256, any parity),
+ * else PITON_EUNSUPPORTED. No reference counterpart: one launch for the chain the reference
+ * runs as three. */
+PITON_API int32_t piton_mi355x_mlp3(const float *x, int64_t M, const float *w1, const float *b1,
+                          const float *w2, const float *b2, const float *w3, const float *b3,
+                          int64_t k0, int64_t n1, int64_t n2, int64_t n3, float *logits,
+                          int32_t *pred, int32_t n_classes, void *stream);
+
 /* piton_mi355x_linear of layer-normalised rows: Y = LN(X) W (+ bias) (ReLU) (+ R), where
  * LN(x) = (x - mean) / sqrt(var + eps) over each row's K columns with the statistics of
  * piton_mi355x_layernorm (the layernorm_kernel of tests/test_reroll_reduce.py:199-208), so the

@@ -1,5 +1,6 @@
-"""The digits MLP chain on the MI355X: three fused dense launches and the argmax of the first
-ten logits (examples/digits_model.py:120-139; tests/test_digits_model.py:102-131).
+"""The digits MLP chain on the MI355X: the three dense layers and the argmax of the first ten
+logits (examples/digits_model.py:120-139; tests/test_digits_model.py:102-131), in one launch
+(mlp3) or one dense launch per layer.
 
 Layers are float32 row-major (w [K, N], b [N]); hidden layers use ReLU. The last layer may be
 the reference's 16-wide padded layer or a plain 10-wide one; predictions use the first
@@ -49,14 +50,21 @@ class MLP:
         self.h = [torch.empty((max_batch, n), device=device) for n in self.sizes[1:]]
         self.pred = torch.empty(max_batch, dtype=torch.int32, device=device)
 
-    def run(self, x: torch.Tensor):
+    def run(self, x: torch.Tensor, fused: bool = True):
         """Logits [M, N_last] and predictions [M] (int32) for float32 x [M, 64] on the GPU;
-        asynchronous on the current stream."""
+        asynchronous on the current stream. A three-layer chain whose sizes fit (even, <= 256)
+        runs as one launch (`mlp3`, the same logits bit for bit); otherwise, or with
+        fused=False, as one dense launch per layer with the argmax fused into the last."""
         M = x.shape[0]
         if M > self.max_batch:
             raise ValueError(f"batch {M} exceeds max_batch {self.max_batch}")
         if not x.is_contiguous():
             raise ValueError("x must be contiguous")
+        if fused and len(self.w) == 3 and all(n <= 256 for n in self.sizes) and all(n % 2 == 0 for n in self.sizes[:3]):
+            out = self.h[-1]
+            rt.mlp3(x, M, self.w[0], self.b[0], self.w[1], self.b[1], self.w[2], self.b[2], out, self.pred,
+                    self.n_classes)
+            return out[:M], self.pred[:M]
         h = x
         last = len(self.w) - 1
         for i, (w, b) in enumerate(zip(self.w, self.b)):

@@ -53,6 +53,7 @@ SIGNATURES = {
     "piton_mi355x_embedding": [_p, _i64, _i64, _p, _p, _p] + [_i64] * 7 + [_p, _p],
     "piton_mi355x_linear": [_p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "piton_mi355x_linear_ln": [_p, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p],
+    "piton_mi355x_mlp3": [_p, _i64] + [_p] * 6 + [_i64] * 4 + [_p, _p, _i32, _p],
     "piton_mi355x_attn_fwd_batched": [_p, _p, _p, _p, _f32] + [_i64] * 16 + [_i32, _i32, _p],
     "piton_mi355x_attn_decode": [_p, _p, _p, _p, _f32] + [_i64] * 13 + [_i32, _p],
     "piton_mi355x_copy": [_p, _p, _i64, _p],
@@ -266,6 +267,26 @@ def linear_ln(x, ldx, eps, w, bias, residual, ldr, y, ldy, M, N, K, relu=False):
     check_tensor("y", y, max_offset=_span((M, ldy), (N, 1)))
     _call("piton_mi355x_linear_ln", _ptr(x), ldx, float(eps), _ptr(w), _ptr(bias), _ptr(residual), ldr, _ptr(y), ldy,
           M, N, K, int(bool(relu)), _stream())
+
+
+def mlp3(x, M, w1, b1, w2, b2, w3, b3, logits, pred, n_classes):
+    """Three dense layers (ReLU on the first two) and the argmax of the first n_classes logits
+    in one launch; logits equal three dense() calls bit for bit. x [M, K0] contiguous."""
+    k0, n1 = w1.shape
+    n2, n3 = w2.shape[1], w3.shape[1]
+    if w2.shape[0] != n1 or w3.shape[0] != n2:
+        raise ValueError(f"mlp3: layer shapes {tuple(w1.shape)}, {tuple(w2.shape)}, {tuple(w3.shape)} do not chain")
+    check_tensor("x", x, max_offset=M * k0 - 1)
+    for name, w, n in (("w1", w1, n1), ("w2", w2, n2), ("w3", w3, n3)):
+        if not w.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        check_tensor(name, w, max_offset=w.numel() - 1)
+    for name, b, n in (("b1", b1, n1), ("b2", b2, n2), ("b3", b3, n3)):
+        check_tensor(name, b, max_offset=n - 1, allow_none=True)
+    check_tensor("logits", logits, max_offset=M * n3 - 1, allow_none=True)
+    check_tensor("pred", pred, dtype=torch.int32, max_offset=M - 1, allow_none=True)
+    _call("piton_mi355x_mlp3", _ptr(x), M, _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(w3), _ptr(b3), k0, n1, n2,
+          n3, _ptr(logits), _ptr(pred), int(n_classes), _stream())
 
 
 def attn_fwd_batched(q, k, v, out, sm_scale, s_qb, s_qh, s_qm, s_kb, s_kh, s_kn, s_kk, s_vb, s_vh, s_vn, s_ob, s_oh,

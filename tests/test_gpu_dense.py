@@ -123,6 +123,29 @@ def test_ragged_batches_reuse_buffers():
         np.testing.assert_allclose(logits.cpu().numpy(), ref, rtol=2e-4, atol=2e-4)
 
 
+@pytest.mark.parametrize("m,sizes", [(1797, (64, 128, 64, 10)), (1797, (64, 128, 64, 16)), (33, (64, 128, 64, 10)),
+                                     (1, (64, 128, 64, 10)), (70, (32, 256, 96, 40))])
+def test_one_launch_chain_equals_three_dense_launches(m, sizes):
+    """mlp3 (the whole chain in one launch) gives the three dense launches' logits and
+    predictions bit for bit: same MFMA chains in the same k order, same epilogues."""
+    layers = digits.he_normal_mlp(seed=m + sizes[-1], sizes=sizes)
+    layers = [(w, np.random.default_rng(i).normal(0, 0.1, b.shape).astype(np.float32)) for i, (w, b) in enumerate(layers)]
+    mlp = digits.MLP(layers, max_batch=m, n_classes=min(10, sizes[-1]))
+    x = torch.from_numpy(np.random.default_rng(m).integers(0, 17, (m, sizes[0])).astype(np.float32)).cuda()
+    lf, pf = (t.clone() for t in mlp.run(x, fused=True))
+    ll, pl = (t.clone() for t in mlp.run(x, fused=False))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(lf.cpu().numpy(), ll.cpu().numpy())
+    np.testing.assert_array_equal(pf.cpu().numpy(), pl.cpu().numpy())
+
+
+def test_one_launch_chain_refuses_unsupported_sizes():
+    w = [torch.zeros(s, device="cuda") for s in ((64, 300), (300, 64), (64, 10))]
+    x = torch.zeros((4, 64), device="cuda")
+    with pytest.raises(rt.MI355XError):
+        rt.mlp3(x, 4, w[0], None, w[1], None, w[2], None, torch.zeros((4, 10), device="cuda"), None, 10)
+
+
 def test_argmax_rows_wide_rows_across_lanes():
     """Rows longer than a wave: ties between lanes go to the first index, the first NaN wins
     wherever it sits, an all -inf row gives 0, row strides are honoured."""

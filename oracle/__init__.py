@@ -17,10 +17,11 @@ exact rational arithmetic truncated toward zero; matmul/dense against dyadic inp
 bit-for-bit), fp64 tolerances and the one-sided truncation bound; exp/exp2/recip/fdiv/sqrt/
 rsqrt against float64 within the reference's tolerances plus special values; softmax and
 attention against float64 plus the reference tests' known answers; layernorm against float64;
-the digits MLP against the reference's known accuracy on its committed model and data.
-Parity unpinned: the last-bit agreement of the emulator's exp/recip/rsqrt sequences with the
-emulator itself (no committed emulator outputs exist; the restatement is checked only to the
-reference's accuracy tolerances and special-value rules).
+the digits MLP against the reference's known accuracy on its committed model and data. And
+bit for bit against the reference's own emulator: golden vectors of exp, exp2, division, division
+by a uniform, 1/x, rsqrt, sqrt (seeded and special values), softmax rows (with +inf, all -inf,
+-inf and NaN rows), the tutorial matmul, attention and the config-1 MLP, written by running the
+reference in the development container (tests/golden/emulator, tests/test_oracle_emulator_vectors.py).
 """
 from __future__ import annotations
 

@@ -1,0 +1,92 @@
+"""The oracle against the reference's own QPU emulator, bit for bit.
+
+tests/golden/emulator/*.npz hold inputs and outputs of the reference's strict emulator
+(written by tests/golden/make_emulator_vectors.py, which imports the reference in the
+development container): one-op math kernels over seeded and special values
+(piton/backend/lower.py: exp/exp2 :2716-2797, division :633-764, rsqrt/sqrt :766-795, 2899-2939),
+softmax_kernel rows with +inf / all -inf / -inf / NaN rows (examples/kernels.py:60-76), the
+tutorial matmul (examples/kernels.py:18-57), attention through run_attention
+(examples/attention.py:200-222) and three dense_layer_kernel launches on config 1
+(examples/nn_kernels.py:23-74). Every output must equal the oracle's bits (NaN equals NaN)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from piton_amd import digits
+
+G = os.path.join(os.path.dirname(__file__), "golden", "emulator")
+
+
+def load(name):
+    return np.load(os.path.join(G, f"{name}.npz"))
+
+
+def assert_bits(got, want):
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    assert got.shape == want.shape
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    bad = np.flatnonzero(~same.ravel())
+    assert bad.size == 0, f"{bad.size} of {same.size} differ, first at {bad[:5]}: " \
+                          f"{got.ravel()[bad[:5]]} vs {want.ravel()[bad[:5]]}"
+
+
+@pytest.mark.parametrize("name,fn", [("exp", oracle.exp), ("exp2", oracle.exp2), ("rsqrt", oracle.rsqrt),
+                                     ("sqrt", oracle.sqrt)])
+def test_unary_math(name, fn):
+    m = load("math")
+    assert_bits(fn(m[f"{name}_x"]), m[f"{name}_y"])
+
+
+def test_one_over_is_division():
+    """`1.0 / x` lowers to the division (a * recip(b) with its NaN rules): 1 / -inf is +0 there
+    (the multiply's zero is +0), while recip alone keeps the sign."""
+    m = load("math")
+    x = m["recip_x"]
+    assert_bits(oracle.fdiv(np.ones_like(x), x), m["recip_y"])
+
+
+def test_division():
+    m = load("math")
+    assert_bits(oracle.fdiv(m["fdiv_x"], m["fdiv_y"]), m["fdiv_out"])
+
+
+@pytest.mark.parametrize("j", range(4))
+def test_division_by_a_uniform(j):
+    m = load("math")
+    x = m["fdiv_uniform_x"]
+    s = np.full_like(x, m[f"fdiv_uniform_s{j}"])
+    assert_bits(oracle.fdiv_uniform(x, s), m[f"fdiv_uniform_out{j}"])
+
+
+@pytest.mark.parametrize("i", range(4))
+def test_softmax_rows(i):
+    s = load("softmax")
+    rows, cols, block, stride = (int(v) for v in s[f"case{i}_shape"])
+    x, want = s[f"case{i}_x"], s[f"case{i}_y"]
+    got = np.asarray(oracle.softmax(x, cols, block))
+    assert_bits(got[:, :cols], want[:, :cols])
+    assert (want[:, cols:] == np.float32(-7.0)).all()  # the kernel leaves the rest of the row
+
+
+@pytest.mark.parametrize("i", range(2))
+def test_matmul(i):
+    m = load("matmul")
+    assert_bits(oracle.matmul(m[f"case{i}_a"], m[f"case{i}_b"]), m[f"case{i}_c"])
+
+
+@pytest.mark.parametrize("i", range(3))
+def test_attention(i):
+    a = load("attention")
+    got = oracle.attention(a[f"case{i}_q"], a[f"case{i}_k"], a[f"case{i}_v"], bool(a[f"case{i}_causal"]), block_n=16)
+    assert_bits(got, a[f"case{i}_o"])
+
+
+def test_config1_mlp_logits_and_predictions():
+    m = load("mlp")
+    layers = digits.he_normal_mlp(seed=1729)
+    chain = [(w, b, i < 2) for i, (w, b) in enumerate(layers)]
+    logits = oracle.mlp_forward(m["x"], chain)
+    assert_bits(logits, m["h3"])
+    np.testing.assert_array_equal(oracle.argmax_rows(logits, 10), m["pred"])

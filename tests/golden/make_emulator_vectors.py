@@ -19,6 +19,10 @@ emulator and writes their inputs and outputs to tests/golden/emulator/*.npz:
                 seed 1729, raw 0..16 pixels) for the first 96 test images, every layer's output
   mlp_full.npz  the same chain's logits and predictions for all 1,797 test images
                 (`--full-mlp`, about half an hour of emulation)
+  softmax_long.npz  softmax_kernel rows at BLOCK_SIZE 1024 and 2048 (n_cols 1000, 1023, 1823),
+                which compile only with the reduction reroll of piton/reroll.py switched on
+                (PITON_REROLL_REDUCE=1, the build of tests/test_reroll_reduce.py:37-44)
+                (`--softmax-long`)
 
 The kernels below are written for this script in the reference's language; no reference source
 is copied anywhere.
@@ -82,10 +86,6 @@ def div_uniform_k(x_ptr, o_ptr, n, s, BLOCK: tl.constexpr):
 SPECIALS = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -1.0, 2.0, 0.5, 4.0, 9.0, 88.7, 88.73, -87.3,
                      -87.4, -103.9, -150.0, 127.9, 128.0, 1e30, -1e30, 3.4e38, 1.17549435e-38, 1.2e-38, 2.0 ** 127,
                      1e-45, -1e-45], np.float32)
-
-
-def run_block(kernel, n, block=128, **kw):
-    kernel[(piton.cdiv(n, block),)](**kw, n=n, BLOCK=block)
 
 
 def math_vectors(rng):
@@ -207,8 +207,38 @@ def mlp_full_vectors():
     return {"logits": h, "pred": np.argmax(h[:, :10], axis=1).astype(np.int32)}
 
 
+def softmax_long_vectors(rng):
+    from kernels import softmax_kernel
+    os.environ["PITON_REROLL_REDUCE"] = "1"
+    sig = {"output_ptr": "*fp32", "input_ptr": "*fp32", "input_row_stride": "i32", "output_row_stride": "i32",
+           "n_cols": "i32"}
+    out = {}
+    cases = [(2, 1000, 1024), (2, 1023, 1024), (2, 1823, 2048)]
+    done = 0
+    for rows, cols, block in cases:
+        try:
+            ck = pc.compile(softmax_kernel, sig, {"BLOCK_SIZE": block}, grid=(rows,))
+        except Exception as e:  # a build the reference cannot make is recorded, not faked
+            print(f"softmax BLOCK {block} n_cols {cols}: no build ({type(e).__name__}: {e})", flush=True)
+            continue
+        x = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
+        y = np.full(rows * cols, np.float32(-7.0))
+        run_emulator(ck, (rows,), {"output_ptr": y, "input_ptr": x.ravel().copy(), "input_row_stride": cols,
+                                   "output_row_stride": cols, "n_cols": cols})
+        out[f"case{done}_x"], out[f"case{done}_y"] = x, y.reshape(rows, cols)
+        out[f"case{done}_shape"] = np.array([rows, cols, block, cols], np.int64)
+        done += 1
+    out["n_cases"] = np.int64(done)
+    return out
+
+
 def main():
     os.makedirs(OUT, exist_ok=True)
+    if "--softmax-long" in sys.argv:
+        t0 = time.time()
+        np.savez_compressed(os.path.join(OUT, "softmax_long.npz"), **softmax_long_vectors(np.random.default_rng(7)))
+        print(f"softmax_long: {time.time() - t0:.1f} s", flush=True)
+        return
     if "--full-mlp" in sys.argv:
         t0 = time.time()
         np.savez_compressed(os.path.join(OUT, "mlp_full.npz"), **mlp_full_vectors())

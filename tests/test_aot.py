@@ -7,7 +7,6 @@ import os
 import shutil
 import subprocess
 
-import numpy as np
 import pytest
 
 from piton_amd import aot

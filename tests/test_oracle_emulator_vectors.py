@@ -4,7 +4,8 @@ tests/golden/emulator/*.npz hold inputs and outputs of the reference's strict em
 (written by tests/golden/make_emulator_vectors.py, which imports the reference in the
 development container): one-op math kernels over seeded and special values
 (piton/backend/lower.py: exp/exp2 :2716-2797, division :633-764, rsqrt/sqrt :766-795, 2899-2939),
-softmax_kernel rows with +inf / all -inf / -inf / NaN rows (examples/kernels.py:60-76), the
+softmax_kernel rows with +inf / all -inf / -inf / NaN rows and rows of 1000-1823 columns at
+BLOCK_SIZE 1024 / 2048 (examples/kernels.py:60-76), the
 tutorial matmul (examples/kernels.py:18-57), attention through run_attention
 (examples/attention.py:200-222) and three dense_layer_kernel launches on config 1
 (examples/nn_kernels.py:23-74). Every output must equal the oracle's bits (NaN equals NaN)."""
@@ -68,6 +69,15 @@ def test_softmax_rows(i):
     got = np.asarray(oracle.softmax(x, cols, block))
     assert_bits(got[:, :cols], want[:, :cols])
     assert (want[:, cols:] == np.float32(-7.0)).all()  # the kernel leaves the rest of the row
+
+
+@pytest.mark.parametrize("i", range(3))
+def test_softmax_long_rows(i):
+    """BLOCK_SIZE 1024 (n_cols 1000, 1023) and 2048 (n_cols 1823, the config's non-power-of-two
+    row), built with the reduction reroll on (tests/test_reroll_reduce.py:37-44)."""
+    s = load("softmax_long")
+    rows, cols, block, _ = (int(v) for v in s[f"case{i}_shape"])
+    assert_bits(np.asarray(oracle.softmax(s[f"case{i}_x"], cols, block)), s[f"case{i}_y"])
 
 
 @pytest.mark.parametrize("i", range(2))

@@ -7,8 +7,8 @@ development container): one-op math kernels over seeded and special values
 softmax_kernel rows with +inf / all -inf / -inf / NaN rows and rows of 1000-1823 columns at
 BLOCK_SIZE 1024 / 2048 (examples/kernels.py:60-76), the
 tutorial matmul (examples/kernels.py:18-57), attention through run_attention
-(examples/attention.py:200-222) and three dense_layer_kernel launches on config 1
-(examples/nn_kernels.py:23-74). Every output must equal the oracle's bits (NaN equals NaN)."""
+(examples/attention.py:200-222) and three dense_layer_kernel launches on config 1, for 96 images and for all
+1,797 (examples/nn_kernels.py:23-74). Every output must equal the oracle's bits (NaN equals NaN)."""
 import os
 
 import numpy as np
@@ -99,4 +99,14 @@ def test_config1_mlp_logits_and_predictions():
     chain = [(w, b, i < 2) for i, (w, b) in enumerate(layers)]
     logits = oracle.mlp_forward(m["x"], chain)
     assert_bits(logits, m["h3"])
+    np.testing.assert_array_equal(oracle.argmax_rows(logits, 10), m["pred"])
+
+
+def test_config1_mlp_all_1797_images():
+    """The emulator's three dense launches over every test image (config 1's whole batch)."""
+    m = load("mlp_full")
+    x = np.load(os.path.join(os.path.dirname(__file__), "golden", "digits", "dataset.npz"))["test_images"]
+    chain = [(w, b, i < 2) for i, (w, b) in enumerate(digits.he_normal_mlp(seed=1729))]
+    logits = oracle.mlp_forward(x.astype(np.float32), chain)
+    assert_bits(logits, m["logits"])
     np.testing.assert_array_equal(oracle.argmax_rows(logits, 10), m["pred"])

@@ -1,6 +1,7 @@
 """Summaries of rocprofv3 output for the benchmark kernels.
 
     python -m piton_amd.profiling KT_DIR FETCH_DIR WRITE_DIR [--json OUT]
+    python -m piton_amd.profiling PMC_DIR --mfma
 
 KT_DIR holds a `--kernel-trace --stats` run of `python3 bench.py` (*_kernel_trace.csv);
 FETCH_DIR / WRITE_DIR hold `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of
@@ -8,6 +9,8 @@ FETCH_DIR / WRITE_DIR hold `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of
 kernel's average duration, and its HBM traffic per launch, each counter scaled by the factor
 that maps the calibration add of known size (bench.py CAL_ELEMS: reads 2 x 256 MiB, writes
 256 MiB) onto its true bytes. --json writes {kernel: {fetch_bytes, write_bytes, ...}}.
+With --mfma, PMC_DIR holds a `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES` run of
+`python3 bench.py --pmc-probe`: the MFMA pipe occupancy of the benchmark's MFMA kernels.
 """
 from __future__ import annotations
 
@@ -89,13 +92,39 @@ def summarize(kt_dir, fetch_dir, write_dir):
     return kernel_stats(kt_dir), traffic, f_fetch, f_write
 
 
+def mfma_busy(pmc_dir, xcds=8, simds=1024):
+    """MFMA pipe occupancy per benchmark MFMA kernel from a
+    `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES` run: SQ_VALU_MFMA_BUSY_CYCLES is summed
+    over the SIMDs and GRBM_GUI_ACTIVE over the XCDs (both as rocprofv3 reports them), so
+    busy = MFMA cycles / (GUI cycles / xcds * simds), a ratio of cycles that does not depend
+    on the clock the kernel ran at."""
+    per = {}
+    for r in csv.DictReader(open(_one(os.path.join(pmc_dir, "*_counter_collection.csv")))):
+        key = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
+        if key not in BENCH or not BENCH[key][2]:
+            continue
+        per.setdefault((key, r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+    out = {}
+    for (key, _), d in per.items():
+        if "GRBM_GUI_ACTIVE" in d and "SQ_VALU_MFMA_BUSY_CYCLES" in d:
+            out.setdefault(key, []).append(d["SQ_VALU_MFMA_BUSY_CYCLES"] / (d["GRBM_GUI_ACTIVE"] / xcds * simds))
+    return {BENCH[k][0]: dict(kernel=k[0], dispatches=len(v), mfma_busy=sum(v) / len(v)) for k, v in out.items()}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("kt_dir")
-    ap.add_argument("fetch_dir")
-    ap.add_argument("write_dir")
+    ap.add_argument("fetch_dir", nargs="?")
+    ap.add_argument("write_dir", nargs="?")
     ap.add_argument("--json")
+    ap.add_argument("--mfma", action="store_true",
+                    help="kt_dir is a --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES run: print MFMA occupancy")
     a = ap.parse_args(argv)
+    if a.mfma:
+        sys.stdout.write("| workload | kernel | dispatches | MFMA pipe busy |\n|---|---|---|---|\n")
+        for label, m in mfma_busy(a.kt_dir).items():
+            sys.stdout.write(f"| {label} | `{m['kernel']}` | {m['dispatches']} | {100 * m['mfma_busy']:.1f} % |\n")
+        return
     stats, traffic, ff, fw = summarize(a.kt_dir, a.fetch_dir, a.write_dir)
     out = sys.stdout
     out.write("## Kernel durations (rocprofv3 --kernel-trace, per dispatch, grouped by grid)\n\n")

@@ -98,6 +98,9 @@ def test_config_random_init_unnormalised_pixels():
     pred, emu_pred, certified = _chain_check(images, layers)
     np.testing.assert_array_equal(pred, emu_pred)
     assert certified.mean() > 0.95  # worst-case bounds; the rest must still agree bit for bit
+    # the reference emulator's own predictions for this batch (tests/golden/emulator/mlp_full.npz)
+    emulator = np.load(os.path.join(os.path.dirname(__file__), "golden", "emulator", "mlp_full.npz"))
+    np.testing.assert_array_equal(pred, emulator["pred"])
 
 
 def test_trained_model_known_accuracy():

@@ -1,0 +1,61 @@
+"""rocprofv3 summaries (piton_amd/profiling.py) on made-up counter files: the calibration scale
+factors of the HBM traffic figures and the MFMA occupancy arithmetic."""
+import csv
+import os
+
+import pytest
+
+from piton_amd import profiling
+
+GEMM = "void piton::gemm_f32_kernel<0, 0, true>(piton::GemmArgs)"
+ADD = "void piton::add_vec4_kernel(float const*, float const*, float*, long)"
+COLS = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value", "Start_Timestamp",
+        "End_Timestamp"]
+
+
+def write_pmc(d, rows):
+    os.makedirs(d, exist_ok=True)
+    with open(os.path.join(d, "run_counter_collection.csv"), "w", newline="") as f:
+        w = csv.DictWriter(f, COLS)
+        w.writeheader()
+        for r in rows:
+            w.writerow(dict(zip(COLS, r)))
+
+
+def write_trace(d, rows):
+    os.makedirs(d, exist_ok=True)
+    with open(os.path.join(d, "run_kernel_trace.csv"), "w", newline="") as f:
+        w = csv.DictWriter(f, ["Kernel_Name", "Grid_Size_X", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        for name, grid, t0, t1 in rows:
+            w.writerow(dict(Kernel_Name=name, Grid_Size_X=grid, Start_Timestamp=t0, End_Timestamp=t1))
+
+
+def test_traffic_is_scaled_by_the_calibration_add(tmp_path):
+    kt, fe, wr = (str(tmp_path / n) for n in ("kt", "fetch", "write"))
+    write_trace(kt, [(GEMM, 262144, 0, 1_000_000), (GEMM, 262144, 0, 1_100_000)])
+    # the counters read half the calibration add's true bytes: the factors are 2
+    write_pmc(fe, [(1, ADD, 64 * 2 ** 20 // 4, "FETCH_SIZE", profiling.CAL_READ / 2 / 1024, 0, 1),
+                   (2, GEMM, 262144, "FETCH_SIZE", 400_000.0, 0, 1)])
+    write_pmc(wr, [(1, ADD, 64 * 2 ** 20 // 4, "WRITE_SIZE", profiling.CAL_WRITE / 2 / 1024, 0, 1),
+                   (2, GEMM, 262144, "WRITE_SIZE", 30_000.0, 0, 1)])
+    stats, traffic, ff, fw = profiling.summarize(kt, fe, wr)
+    assert ff == pytest.approx(2.0) and fw == pytest.approx(2.0)
+    t = traffic["matmul 4096^3"]
+    assert t["fetch_bytes"] == pytest.approx(2 * 400_000 * 1024)
+    assert t["write_bytes"] == pytest.approx(2 * 30_000 * 1024)
+    assert t["algorithmic_bytes"] == 3 * 4096 * 4096 * 4
+    assert stats[0]["calls"] == 2 and stats[0]["avg_ns"] == pytest.approx(1_050_000)
+
+
+def test_mfma_busy(tmp_path):
+    d = str(tmp_path / "pmc")
+    # 1 ms at 2.4 GHz on each of 8 XCDs; the 1024 SIMDs' MFMA pipes busy 90 % of it
+    gui = 8 * 2.4e6
+    busy = 0.9 * 2.4e6 * 1024
+    write_pmc(d, [(7, GEMM, 262144, "GRBM_GUI_ACTIVE", gui, 5_000, 1_005_000),
+                  (7, GEMM, 262144, "SQ_VALU_MFMA_BUSY_CYCLES", busy, 5_000, 1_005_000),
+                  (8, ADD, 1024, "GRBM_GUI_ACTIVE", 100.0, 0, 10)])
+    m = profiling.mfma_busy(d)
+    assert list(m) == ["matmul 4096^3"]
+    assert m["matmul 4096^3"]["mfma_busy"] == pytest.approx(0.9)

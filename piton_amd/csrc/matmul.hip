@@ -321,7 +321,17 @@ void gemm_f32_kernel(GemmArgs g) {
 // three workgroups per CU. At 4096^3 this runs ~5 % faster than the LDS kernel, whose two
 // barriers per K tile left the matrix pipe idle 14 % of the time; at four workgroups per CU
 // (128 VGPRs) it spills and runs 10 % slower.
-__global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(3)))
+#ifndef PITON_GEMM_DIRECT_KT
+#define PITON_GEMM_DIRECT_KT 32
+#endif
+#ifndef PITON_GEMM_DIRECT_WAVES
+#define PITON_GEMM_DIRECT_WAVES 3
+#endif
+// K per register tile: 32 (144 VGPRs, three workgroups per CU) and 16 (114 VGPRs, four per
+// CU) measured the same; 32 is the default
+constexpr int DKT = PITON_GEMM_DIRECT_KT;
+constexpr int DKH = DKT / 2;               // k per lane half per tile
+__global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(PITON_GEMM_DIRECT_WAVES)))
 void gemm_direct_kernel(GemmArgs g) {
     const int t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63;
@@ -346,25 +356,25 @@ void gemm_direct_kernel(GemmArgs g) {
     uint32_t va[2], vb[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        va[i] = (uint32_t)(((m0 + wm * 64 + i * 32 + l31) * g.s_am + 16 * half) * 4);
-        vb[i] = (uint32_t)(((int64_t)(16 * half) * g.s_bk + n0 + wn * 64 + i * 32 + l31) * 4);
+        va[i] = (uint32_t)(((m0 + wm * 64 + i * 32 + l31) * g.s_am + DKH * half) * 4);
+        vb[i] = (uint32_t)(((int64_t)(DKH * half) * g.s_bk + n0 + wn * 64 + i * 32 + l31) * 4);
     }
     const uint32_t sbk4 = (uint32_t)(g.s_bk * 4);
 
     struct Ops {
-        f32x4 a[2][4];
-        float b[2][16];
+        f32x4 a[2][DKH / 4];
+        float b[2][DKH];
     };
     auto load = [&](int kt, Ops &o) {
-        const int ka = kt * (GBK * 4);
-        const int kb = (int)((uint32_t)kt * GBK * sbk4);
+        const int ka = kt * (DKT * 4);
+        const int kb = (int)((uint32_t)kt * DKT * sbk4);
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+            for (int q = 0; q < DKH / 4; q++)
                 o.a[i][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(va[i] + 16 * q), ka, 0));
 #pragma unroll
-        for (int s = 0; s < 16; s++)
+        for (int s = 0; s < DKH; s++)
 #pragma unroll
             for (int i = 0; i < 2; i++)
                 o.b[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)vb[i], kb + s * (int)sbk4, 0));
@@ -378,16 +388,16 @@ void gemm_direct_kernel(GemmArgs g) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
     auto mul = [&](const Ops &o) {
 #pragma unroll
-        for (int s = 0; s < 16; s++)
+        for (int s = 0; s < DKH; s++)
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i][s >> 2][s & 3], o.b[j][s], acc[i][j], 0, 0, 0);
     };
-    // K % 64 == 0: the tiles come in pairs; the last pair's prefetch reads past K, which the
+    // K % (2 DKT) == 0: the tiles come in pairs; the last pair's prefetch reads past K, which the
     // descriptors turn into zeros that are never used
-    const int nk = (int)(g.K / GBK);
+    const int nk = (int)(g.K / DKT);
     Ops o0, o1;
     load(0, o0);
     for (int kt = 0; kt < nk; kt += 2) {
@@ -600,7 +610,7 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
     const int al = layout_a(g), bl = layout_b(g);
     const int nwg = (int)tiles;
     const bool whole = al == VEC_ROW && bl == VEC_ROW && g.M % GBM == 0 && g.N % GBN == 0 && g.K % GBK == 0 && g.K > 0;
-    if (PITON_GEMM_DIRECT && whole && g.K % (2 * GBK) == 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) &&
+    if (PITON_GEMM_DIRECT && whole && g.K % (2 * DKT) == 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) &&
         (g.K - 1) * g.s_bk + g.N < (1LL << 29))
         hipLaunchKernelGGL(gemm_direct_kernel, dim3(nwg), dim3(GTHREADS), 0, st, g);
     else if (whole)

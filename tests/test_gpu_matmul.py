@@ -120,10 +120,14 @@ def test_numpy_arrays_copy_in_copy_out():
     np.testing.assert_array_equal(b, b0)
 
 
-@pytest.mark.parametrize("M,N,K,pad", [(256, 384, 96, (4, 8, 3)), (128, 128, 32, (0, 0, 0)), (384, 128, 2080, (8, 4, 1))])
+@pytest.mark.parametrize("M,N,K,pad", [(256, 384, 96, (4, 8, 3)), (128, 128, 32, (0, 0, 0)), (384, 128, 2080, (8, 4, 1)),
+                                       (256, 384, 128, (4, 8, 3)), (128, 128, 64, (0, 0, 0)),
+                                       (384, 256, 2112, (8, 4, 1))])
 def test_whole_tile_shapes_with_padded_rows(M, N, K, pad):
-    """Shapes whose tiles are all whole (M, N multiples of 128, K of 32) take the unguarded
-    kernel: padded row strides of A, B and C must not leak into the product or past C's rows."""
+    """Shapes whose tiles are all whole (M, N multiples of 128) take the unguarded kernels: the
+    register-direct one for K % 64 == 0, whose last prefetch reads past K, and the LDS one's
+    whole-tile instantiation for K % 32 == 0. Padded row strides of A, B and C (NaN in the
+    padding) must not leak into the product or past C's rows."""
     rng = np.random.default_rng(M + N + K)
     a = dyadic(rng, (M, K))
     b = dyadic(rng, (K, N))
@@ -148,6 +152,14 @@ def test_group_order_does_not_change_bits(group):
     base = run(a, b, group=8)
     other = run(a, b, group=group)
     assert torch.equal(base, other)
+
+
+@pytest.mark.parametrize("group", [1, 3, 64])
+def test_group_order_does_not_change_bits_whole_tiles(group):
+    g = torch.Generator(device="cuda").manual_seed(12)
+    a = torch.rand((640, 256), device="cuda", generator=g)
+    b = torch.rand((256, 896), device="cuda", generator=g)
+    assert torch.equal(run(a, b, group=8), run(a, b, group=group))
 
 
 def test_empty_and_k_zero():

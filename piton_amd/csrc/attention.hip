@@ -708,6 +708,111 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs g) {
     }
 }
 
+// Short caches (n_keys <= 256, head_dim <= 64: a decoder with a small context): the same
+// arithmetic in the same order as attn_decode_kernel, so the two give identical bits, but every
+// K and V element the workgroup needs is requested before any of it is used: one memory round
+// trip instead of one per key chunk plus a chain of V loads behind the softmax.
+constexpr int kShortDecodeKeys = 256;
+#ifndef PITON_DECODE_SHORT
+#define PITON_DECODE_SHORT 1
+#endif
+
+template <int D, bool VEC>
+__global__ __launch_bounds__(256) void attn_decode_short(DecodeArgs g) {
+    static_assert(D <= 64, "short decode holds K and V in registers for head_dim <= 64");
+    __shared__ float p[kShortDecodeKeys];
+    __shared__ float red[8];
+    __shared__ float part[256];
+    constexpr int TPK = D / 16, KPP = 256 / TPK, KG = 256 / D;
+    constexpr int NIT = kShortDecodeKeys / KPP, NV = kShortDecodeKeys / KG;
+    const int t = threadIdx.x;
+    const int64_t bh = blockIdx.x, b = bh / g.n_heads, h = bh % g.n_heads;
+    const float *qp = g.q + b * g.s_qb + h * g.s_qh;
+    const float *kp = g.k + b * g.s_kb + h * g.s_kh;
+    const float *vp = g.v + b * g.s_vb + h * g.s_vh;
+    const int n_keys = g.n_keys, head_dim = g.head_dim;
+    const int sub = t % TPK, kslot = t / TPK, d0 = 16 * sub;
+    const bool dims_ok = d0 < head_dim;
+    const int d = t % D, kg = t / D;
+    const bool d_ok = d < head_dim;
+
+    f32x4 kv[NIT][4];
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int j = it * KPP + kslot;
+        const float *kr = kp + (int64_t)j * g.s_kn + d0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            f32x4 f = {0.f, 0.f, 0.f, 0.f};
+            if (j < n_keys && dims_ok) {
+                if constexpr (VEC) f = *reinterpret_cast<const f32x4 *>(kr + 4 * c);
+                else f = f32x4{kr[4 * c], kr[4 * c + 1], kr[4 * c + 2], kr[4 * c + 3]};
+            }
+            kv[it][c] = f;
+        }
+    }
+    // V through a descriptor bounded at the last key's row: rows past it read as zeros, so the
+    // loads need no per-key predicate. The whole offset is the per-lane one (the descriptor's
+    // range check does not cover `soffset`); the host checks it fits 31 bits.
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(vp), (short)0,
+                                                      (int)(((int64_t)(n_keys - 1) * g.s_vn + head_dim) * 4), 0x00020000);
+    const int vo = (int)((d + (int64_t)kg * g.s_vn) * 4), vstep = (int)(KG * g.s_vn * 4);
+    float vv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+        vv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, vo + i * vstep, 0, 0));
+    float q16[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) q16[i] = dims_ok ? qp[d0 + i] * g.scale : 0.f;
+
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int j = it * KPP + kslot;
+        float sc = 0.f;
+        if (j < n_keys && dims_ok) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                sc = fmaf(q16[4 * c], kv[it][c][0], sc);
+                sc = fmaf(q16[4 * c + 1], kv[it][c][1], sc);
+                sc = fmaf(q16[4 * c + 2], kv[it][c][2], sc);
+                sc = fmaf(q16[4 * c + 3], kv[it][c][3], sc);
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < TPK; o <<= 1) sc += __shfl_xor(sc, o);
+        if (j < n_keys) {
+            if (sub == 0) p[j] = sc;
+            mloc = fmaxf(mloc, sc);
+        }
+    }
+    for (int j = n_keys + t; j < kShortDecodeKeys; j += 256) p[j] = 0.f;  // weights of absent keys
+    const float m = block_reduce4(mloc, MaxOp(), red);
+    float lsum = 0.f;
+    for (int j = t; j < n_keys; j += 256) {
+        const float e = __builtin_amdgcn_exp2f(p[j] - m);
+        p[j] = e;
+        lsum += e;
+    }
+    const float inv = 1.0f / block_reduce4(lsum, SumOp(), red + 4);
+
+    // keys past n_keys add fmaf(+0, +0, acc) = acc (acc starts at +0 and never becomes -0), so
+    // the sum equals attn_decode_kernel's, which skips them
+    float acc = 0.f;
+    if (d_ok) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) acc = fmaf(p[kg + KG * i], vv[i], acc);
+    }
+    part[t] = acc;
+    __syncthreads();
+    if (t < D && t < head_dim) {
+        float v = part[t];
+#pragma unroll
+        for (int w = 1; w < KG; w++) v += part[w * D + t];
+        g.o[b * g.s_ob + h * g.s_oh + t] = v * inv;
+    }
+}
+
 static int attn_launch(AttnArgs g, int64_t batch, int64_t n_heads, int32_t head_dim, hipStream_t st) {
     g.q_vec = aligned16(g.q) && g.s_qm % 4 == 0 && g.s_qh % 4 == 0 && g.s_qb % 4 == 0 && head_dim % 4 == 0;
     g.v_vec = aligned16(g.v) && g.s_vn % 4 == 0 && g.s_vh % 4 == 0 && g.s_vb % 4 == 0 && head_dim % 4 == 0;
@@ -822,14 +927,19 @@ int32_t piton_mi355x_attn_decode(const float *q, const float *k, const float *v,
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)(batch * n_heads)), block(256);
     const bool vec = aligned16(k) && stride_kn % 4 == 0 && stride_kh % 4 == 0 && stride_kb % 4 == 0;
-#define PITON_DEC(D)                                                                                                \
+#define PITON_DEC(KERNEL, D)                                                                                        \
     do {                                                                                                            \
-        if (vec) hipLaunchKernelGGL((attn_decode_kernel<D, true>), grid, block, 0, st, g);                          \
-        else hipLaunchKernelGGL((attn_decode_kernel<D, false>), grid, block, 0, st, g);                             \
+        if (vec) hipLaunchKernelGGL((KERNEL<D, true>), grid, block, 0, st, g);                                      \
+        else hipLaunchKernelGGL((KERNEL<D, false>), grid, block, 0, st, g);                                         \
     } while (0)
-    if (head_dim <= 32) PITON_DEC(32);
-    else if (head_dim == 64) PITON_DEC(64);
-    else PITON_DEC(128);
+    // short caches: every V offset the kernel forms (up to 256 rows and 64 dims) within 31 bits
+    const bool short_cache = PITON_DECODE_SHORT && n_keys <= kShortDecodeKeys && stride_vn >= 0 &&
+                             ((int64_t)kShortDecodeKeys * stride_vn + 64) * 4 < 0x7FFFFFFF;
+    if (head_dim <= 32 && short_cache) PITON_DEC(attn_decode_short, 32);
+    else if (head_dim == 64 && short_cache) PITON_DEC(attn_decode_short, 64);
+    else if (head_dim <= 32) PITON_DEC(attn_decode_kernel, 32);
+    else if (head_dim == 64) PITON_DEC(attn_decode_kernel, 64);
+    else PITON_DEC(attn_decode_kernel, 128);
 #undef PITON_DEC
     rc = check_launch("attn_decode");
     if (rc == PITON_OK) clear_error();

@@ -317,7 +317,8 @@ void gemm_f32_kernel(GemmArgs g) {
 // makes each lane's A operands 16 consecutive floats of its row (four 16-byte loads) and its
 // B operands 16 rows of its column (one 4-byte load per row, 128 contiguous bytes per
 // half-wave). Operands of tile k+1 are loaded while tile k multiplies (two register sets,
-// the loop unrolled by two). Buffer descriptors carry the matrices (each < 2 GiB). 144 VGPRs:
+// the loop unrolled by two). Buffer descriptors carry the matrices (each < 2 GiB); every load
+// lies inside them. 144 VGPRs:
 // three workgroups per CU. At 4096^3 this runs ~5 % faster than the LDS kernel, whose two
 // barriers per K tile left the matrix pipe idle 14 % of the time; at four workgroups per CU
 // (128 VGPRs) it spills and runs 10 % slower.
@@ -395,15 +396,17 @@ void gemm_direct_kernel(GemmArgs g) {
                 for (int j = 0; j < 2; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i][s >> 2][s & 3], o.b[j][s], acc[i][j], 0, 0, 0);
     };
-    // K % (2 DKT) == 0: the tiles come in pairs; the last pair's prefetch reads past K, which the
-    // descriptors turn into zeros that are never used
+    // K % (2 DKT) == 0: the tiles come in pairs. The last pair's prefetch loads the last tile
+    // again (never used) rather than a tile past K: every load stays inside the matrices, which
+    // also keeps the uniform offsets in `soffset` legal (the descriptor's range check covers the
+    // per-lane offset only)
     const int nk = (int)(g.K / DKT);
     Ops o0, o1;
     load(0, o0);
     for (int kt = 0; kt < nk; kt += 2) {
         load(kt + 1, o1);
         mul(o0);
-        load(kt + 2, o0);
+        load(min(kt + 2, nk - 1), o0);
         mul(o1);
     }
 

@@ -128,7 +128,7 @@ def test_position_major_attention_prefill_and_decode():
 
 
 @pytest.mark.parametrize("dh,n_keys,pad", [(16, 3, 0), (32, 1, 0), (64, 257, 0), (128, 1000, 0), (64, 300, 1),
-                                           (128, 8192, 0)])
+                                           (128, 8192, 0), (64, 256, 0), (64, 200, 1), (32, 256, 0), (16, 130, 1)])
 def test_decode_attention_head_dims_and_long_caches(dh, n_keys, pad):
     """One query per (batch, head) against n_keys cached keys, [B, H, N, Dh] caches with a row
     padding of `pad` floats (pad = 1 takes the scalar-load path), up to the 8192-key limit."""
@@ -148,6 +148,51 @@ def test_decode_attention_head_dims_and_long_caches(dh, n_keys, pad):
     got = out.cpu().numpy()
     assert fp64.rel_fro(got[..., :dh], ref) <= 1e-5
     assert (got[..., dh:] == -9.0).all()
+
+
+def _decode(q, k, v, n_keys):
+    """attn_decode over [B, H, rows, Dh] caches (rows >= n_keys), contiguous."""
+    B, H, rows, dh = k.shape
+    tq, tk, tv = (torch.from_numpy(np.ascontiguousarray(t)).cuda() for t in (q, k, v))
+    out = torch.zeros((B, H, dh), device="cuda")
+    rt.attn_decode(tq, tk, tv, out, 1 / 8, H * dh, dh, H * rows * dh, rows * dh, dh, H * rows * dh, rows * dh, dh,
+                   H * dh, dh, n_keys, B, H, dh)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("n_keys", [1, 100, 255, 256])
+def test_decode_ignores_cache_rows_past_n_keys(n_keys):
+    """Rows of the cache past n_keys (NaN here) are never read: the result equals the one from a
+    cache of exactly n_keys rows, bit for bit."""
+    rng = np.random.default_rng(n_keys)
+    B, H, dh, cap = 2, 4, 64, 300
+    q = rng.standard_normal((B, H, dh)).astype(np.float32)
+    k = np.full((B, H, cap, dh), np.nan, np.float32)
+    v = np.full((B, H, cap, dh), np.nan, np.float32)
+    k[:, :, :n_keys] = rng.standard_normal((B, H, n_keys, dh))
+    v[:, :, :n_keys] = rng.standard_normal((B, H, n_keys, dh))
+    got = _decode(q, k, v, n_keys)
+    assert np.isfinite(got).all()
+    exact = _decode(q, k[:, :, :n_keys], v[:, :, :n_keys], n_keys)
+    np.testing.assert_array_equal(got.view(np.uint32), exact.view(np.uint32))
+
+
+@pytest.mark.parametrize("dh", [32, 64])
+def test_short_and_long_decode_kernels_agree(dh):
+    """Caches of up to 256 keys take the kernel that requests all of K and V up front, longer ones
+    the chunked kernel; their arithmetic is the same. A 257th key whose score is -inf adds
+    exactly zero to the sum and to P V, so 257 keys on the long kernel give the bits of the
+    first 256 on the short one."""
+    rng = np.random.default_rng(dh)
+    B, H = 3, 2
+    q = np.abs(rng.standard_normal((B, H, dh))).astype(np.float32) + np.float32(0.1)
+    k = rng.standard_normal((B, H, 257, dh)).astype(np.float32)
+    v = rng.standard_normal((B, H, 257, dh)).astype(np.float32)
+    k[:, :, 256] = -np.inf  # positive q: the score is -inf
+    short = _decode(q, k[:, :, :256], v[:, :, :256], 256)
+    long_ = _decode(q, k, v, 257)
+    np.testing.assert_array_equal(short.view(np.uint32), long_.view(np.uint32))
 
 
 def test_strided_embedding_and_bad_ids():

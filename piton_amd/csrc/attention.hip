@@ -367,8 +367,8 @@ __device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 //     a conflict-free LDS read instead of 32 registers per lane;
 //   * V blocks are copied from memory straight into the wave's LDS slab (16-byte LDS-DMA);
 //   * software pipeline: block j+1's score product is issued beside block j's exps, K is loaded
-//     two blocks ahead and V one block ahead; the first block's K and V are requested before
-//     Q is staged, so those latencies overlap;
+//     two blocks ahead and V one block ahead; Q is requested first and the first block's K
+//     and V right after it, so the Q staging overlaps their latency;
 //   * PAIR (causal): the workgroup runs query group nqg-1-p, then group p, so each workgroup
 //     visits nqg + 1 key blocks. A wave parks its first group's state in registers and the
 //     pipeline runs on into the second group without a barrier; both merge at the end;
@@ -380,6 +380,10 @@ __device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 // workgroups per CU (one generation)
 #ifndef PITON_ATTN_PAIR_MODE
 #define PITON_ATTN_PAIR_MODE 2
+#endif
+// Q staging: Q requested before the first K/V block and unrolled (1), or after them (0)
+#ifndef PITON_ATTN_Q_FIRST
+#define PITON_ATTN_Q_FIRST 1
 #endif
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
@@ -512,19 +516,61 @@ void attn_fwd_fast(AttnArgs g) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)&vw[KPC * c][0], 16, off + v_c * c, 0, 0, 0);
     };
 
+    // Q'^T of the groups: qT[gi][d][j] = Q[qg_gi*AQG + j][d] * sm_scale * log2 e (rows past
+    // n_ctx: 0). Every Q chunk is requested first, then the first block's K and V: the memory
+    // counter is in order, so the Q writes wait for Q alone while K and V are still in flight.
+    // Every wave requests a first block (one without blocks requests block `wave`, never used).
+    constexpr int QIT = NG * AQG * D / 4 / (64 * ANW);
+    static_assert(NG * AQG * D / 4 % (64 * ANW) == 0, "whole Q chunks per thread");
+    auto q_chunk = [&](int c, int &gi, int &j, int &dq) {
+        const int i = t + 64 * ANW * c, r = i % (AQG * D / 4);
+        gi = i / (AQG * D / 4);
+        j = r / (D / 4);
+        dq = r % (D / 4);
+    };
     float kf[D / 2];
+#if PITON_ATTN_Q_FIRST
+    f32x4 qv[QIT];
+#pragma unroll
+    for (int c = 0; c < QIT; c++) {
+        int gi, j, dq;
+        q_chunk(c, gi, j, dq);
+        qv[c] = bload4(rq, ((uint32_t)((gi ? qg1 : qg0) * AQG + j) * s_qm + 4 * dq) * 4u);
+    }
+    load_k(kf, kb_of(0));
+    fetch_v(kb_of(0));
+#pragma unroll
+    for (int c = 0; c < QIT; c++) {
+        int gi, j, dq;
+        q_chunk(c, gi, j, dq);
+#pragma unroll
+        for (int e = 0; e < 4; e++) qT[gi][4 * dq + e][j] = qv[c][e] * g.scale;
+    }
+#else
     if (n > 0) {  // the first block's K and V are in flight while Q is staged
         load_k(kf, kb_of(0));
         fetch_v(kb_of(0));
     }
-    // Q'^T of the groups: qT[gi][d][j] = Q[qg_gi*AQG + j][d] * sm_scale * log2 e (rows past n_ctx: 0)
-    for (int i = t; i < NG * AQG * D / 4; i += 64 * ANW) {
-        const int gi = i / (AQG * D / 4), r = i % (AQG * D / 4), j = r / (D / 4), dq = r % (D / 4);
+    for (int c = 0; c < QIT; c++) {
+        int gi, j, dq;
+        q_chunk(c, gi, j, dq);
         const f32x4 f = bload4(rq, ((uint32_t)((gi ? qg1 : qg0) * AQG + j) * s_qm + 4 * dq) * 4u);
 #pragma unroll
         for (int e = 0; e < 4; e++) qT[gi][4 * dq + e][j] = f[e] * g.scale;
     }
+#endif
+#if PITON_ATTN_Q_FIRST
+    // the other waves need the Q tiles only: wait for this wave's LDS writes and meet at the
+    // barrier, without the release fence of __syncthreads, which would also wait for the
+    // first block's V copy into this wave's own slab (its wave waits for that in the loop)
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    __builtin_amdgcn_sched_barrier(0);
+#else
     __syncthreads();
+#endif
 
     f32x16 o[D / 32], po[D / 32];  // the running state and (PAIR) the parked first group's
 #pragma unroll
@@ -594,6 +640,8 @@ void attn_fwd_fast(AttnArgs g) {
         xm[wave][0][lane] = sm;
         xm[wave][1][lane] = sl;
     };
+    // a wave without blocks still has its first block's V copy in flight into its slab
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();  // every wave is done with its slab and the Q tiles
     const bool second = PAIR && n1 > 0;  // the running state is the second group's
     put(second ? 1 : 0, o, m_i, l_i);

@@ -613,8 +613,10 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
     const int al = layout_a(g), bl = layout_b(g);
     const int nwg = (int)tiles;
     const bool whole = al == VEC_ROW && bl == VEC_ROW && g.M % GBM == 0 && g.N % GBN == 0 && g.K % GBK == 0 && g.K > 0;
-    if (PITON_GEMM_DIRECT && whole && g.K % (2 * DKT) == 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) &&
-        (g.K - 1) * g.s_bk + g.N < (1LL << 29))
+    // the direct kernel addresses rows by 32-bit byte offsets from the matrix base: positive row
+    // strides and every element within 2^31 bytes
+    if (PITON_GEMM_DIRECT && whole && g.K % (2 * DKT) == 0 && g.s_am > 0 && g.s_bk > 0 &&
+        (g.M - 1) * g.s_am + g.K < (1LL << 29) && (g.K - 1) * g.s_bk + g.N < (1LL << 29))
         hipLaunchKernelGGL(gemm_direct_kernel, dim3(nwg), dim3(GTHREADS), 0, st, g);
     else if (whole)
         hipLaunchKernelGGL((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);

@@ -3,6 +3,8 @@
 Bar: bit-exact on dyadic inputs (every product and partial sum exact, so any order gives the
 same bits; tests/test_nn_kernels.py:37-61 style); otherwise relative Frobenius error <= 1e-5
 vs float64 and no larger than the oracle's (the emulator's round-toward-zero chain)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -160,6 +162,22 @@ def test_group_order_does_not_change_bits_whole_tiles(group):
     a = torch.rand((640, 256), device="cuda", generator=g)
     b = torch.rand((256, 896), device="cuda", generator=g)
     assert torch.equal(run(a, b, group=8), run(a, b, group=group))
+
+
+@pytest.mark.parametrize("K", [128, 96])
+def test_negative_row_stride_through_the_c_abi(K):
+    """The C entry takes any strides: A addressed from its last row with row stride -K (a
+    row-reversed view) on a whole-tile shape gives the product of the reversed rows."""
+    M, N = 256, 256
+    rng = np.random.default_rng(K)
+    a = dyadic(rng, (M, K))
+    b = dyadic(rng, (K, N))
+    ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    tc = torch.full((M, N), -1.0, device="cuda")
+    last_row = ctypes.c_void_p(ta.data_ptr() + (M - 1) * K * 4)
+    rt._call("piton_mi355x_matmul", last_row, rt._ptr(tb), rt._ptr(tc), M, N, K, -K, 1, N, 1, N, 1, 8, rt._stream())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(tc.cpu().numpy(), a[::-1] @ b)
 
 
 def test_empty_and_k_zero():

@@ -164,6 +164,46 @@ def test_group_order_does_not_change_bits_whole_tiles(group):
     assert torch.equal(run(a, b, group=8), run(a, b, group=group))
 
 
+def _sweep_shape(rng, kind):
+    if kind == 0:  # whole tiles, K % 64 == 0: the register-direct kernel
+        return int(rng.integers(1, 5)) * 128, int(rng.integers(1, 5)) * 128, int(rng.integers(1, 11)) * 64
+    if kind == 1:  # whole tiles, K % 32 == 0: the direct kernel or the LDS kernel's whole-tile form
+        return int(rng.integers(1, 5)) * 128, int(rng.integers(1, 5)) * 128, int(rng.integers(1, 21)) * 32
+    return tuple(int(rng.integers(1, 400)) for _ in range(3))  # ragged edges
+
+
+def test_seeded_shape_sweep_against_float64():
+    """48 seeded shapes and layouts in one process (whole tiles for the register-direct and the
+    LDS kernels, ragged edges, padded rows, A or B stored transposed); every element within the
+    worst-case bound of a float32 contraction in any order, |C - C64| <= (K + 2) u sum_k |A||B|,
+    u = 2^-24."""
+    rng = np.random.default_rng(2026)
+    for case in range(48):
+        kind = case % 4
+        M, N, K = _sweep_shape(rng, kind)
+        a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+        b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        pad_a = int(rng.integers(0, 3)) * 4 if kind < 2 else int(rng.integers(0, 5))
+        pad_b = int(rng.integers(0, 3)) * 4 if kind < 2 else int(rng.integers(0, 5))
+        if kind == 3 and case % 8 == 3:  # A stored transposed: element (m, k) at k * M + m
+            A = torch.from_numpy(np.ascontiguousarray(a.T)).cuda().t()
+        else:
+            A = torch.zeros((M, K + pad_a), device="cuda")
+            A[:, :K] = torch.from_numpy(a).cuda()
+            A = A[:, :K]
+        if kind == 3 and case % 8 == 7:  # B stored transposed
+            B = torch.from_numpy(np.ascontiguousarray(b.T)).cuda().t()
+        else:
+            B = torch.zeros((K, N + pad_b), device="cuda")
+            B[:, :N] = torch.from_numpy(b).cuda()
+            B = B[:, :N]
+        got = run(A, B).cpu().numpy()
+        ref = fp64.matmul(a, b)
+        bound = (K + 2) * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+        bad = np.abs(got - ref) > bound
+        assert not bad.any(), (case, M, N, K, pad_a, pad_b, int(bad.sum()))
+
+
 @pytest.mark.parametrize("K", [128, 96])
 def test_negative_row_stride_through_the_c_abi(K):
     """The C entry takes any strides: A addressed from its last row with row stride -K (a

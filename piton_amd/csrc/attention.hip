@@ -368,7 +368,7 @@ __device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 //   * V blocks are copied from memory straight into the wave's LDS slab (16-byte LDS-DMA);
 //   * software pipeline: block j+1's score product is issued beside block j's exps, K is loaded
 //     two blocks ahead and V one block ahead; Q is requested first and the first block's K
-//     and V right after it, so the Q staging overlaps their latency;
+//     right after it, so the Q staging overlaps its latency; the first V follows the barrier;
 //   * PAIR (causal): the workgroup runs query group nqg-1-p, then group p, so each workgroup
 //     visits nqg + 1 key blocks. A wave parks its first group's state in registers and the
 //     pipeline runs on into the second group without a barrier; both merge at the end;
@@ -517,9 +517,9 @@ void attn_fwd_fast(AttnArgs g) {
     };
 
     // Q'^T of the groups: qT[gi][d][j] = Q[qg_gi*AQG + j][d] * sm_scale * log2 e (rows past
-    // n_ctx: 0). Every Q chunk is requested first, then the first block's K and V: the memory
-    // counter is in order, so the Q writes wait for Q alone while K and V are still in flight.
-    // Every wave requests a first block (one without blocks requests block `wave`, never used).
+    // n_ctx: 0). Every Q chunk is requested first, then the first block's K: the memory counter
+    // is in order, so the Q writes wait for Q alone while K is still in flight. Every wave
+    // requests a first K block (one without blocks requests block `wave`, never used).
     constexpr int QIT = NG * AQG * D / 4 / (64 * ANW);
     static_assert(NG * AQG * D / 4 % (64 * ANW) == 0, "whole Q chunks per thread");
     auto q_chunk = [&](int c, int &gi, int &j, int &dq) {
@@ -538,7 +538,6 @@ void attn_fwd_fast(AttnArgs g) {
         qv[c] = bload4(rq, ((uint32_t)((gi ? qg1 : qg0) * AQG + j) * s_qm + 4 * dq) * 4u);
     }
     load_k(kf, kb_of(0));
-    fetch_v(kb_of(0));
 #pragma unroll
     for (int c = 0; c < QIT; c++) {
         int gi, j, dq;
@@ -561,8 +560,8 @@ void attn_fwd_fast(AttnArgs g) {
 #endif
 #if PITON_ATTN_Q_FIRST
     // the other waves need the Q tiles only: wait for this wave's LDS writes and meet at the
-    // barrier, without the release fence of __syncthreads, which would also wait for the
-    // first block's V copy into this wave's own slab (its wave waits for that in the loop)
+    // barrier, without the release fence of __syncthreads, whose wait covers every memory
+    // operation in flight (the first block's K, which only this wave reads, included)
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
@@ -580,6 +579,11 @@ void attn_fwd_fast(AttnArgs g) {
     float m_i = -INFINITY, l_i = 0.f, pm = -INFINITY, pl = 0.f;
 
     if (n > 0) {
+#if PITON_ATTN_Q_FIRST
+        // the first block's V after the start-up burst of Q and K (it is needed only after the
+        // first scores and exps), and before block 1's K, as the loop's waits assume
+        fetch_v(kb_of(0));
+#endif
         f32x16 st = block_scores_lds<D>(kf, qT[0], half, l31);
         // the loop starts with the next block's K issued before this block's V is waited for,
         // the order it keeps every iteration, so each wait on K lets newer V loads stay in flight
@@ -640,7 +644,7 @@ void attn_fwd_fast(AttnArgs g) {
         xm[wave][0][lane] = sm;
         xm[wave][1][lane] = sl;
     };
-    // a wave without blocks still has its first block's V copy in flight into its slab
+    // every V copy into the slabs has landed before the LDS is reused for the merge
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();  // every wave is done with its slab and the Q tiles
     const bool second = PAIR && n1 > 0;  // the running state is the second group's

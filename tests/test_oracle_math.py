@@ -4,7 +4,7 @@ accuracy tests and special values (tests/test_tiles.py:158-228), the reference's
 for x / 1.0 (tests/test_attention.py:25-27), and the claim that fdiv_uniform gives fdiv's
 bits (lower.py:736-739). A dropped polynomial term, a wrong constant or a wrong special-case
 rule fails one of these; the last-bit agreement of the sequences with the emulator itself is
-not pinned (no emulator outputs are committed anywhere)."""
+pinned separately by the emulator's own outputs (tests/test_oracle_emulator_vectors.py)."""
 import numpy as np
 import pytest
 

@@ -252,7 +252,7 @@ def cpu_baseline(a, b, budget_s=10.0):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build",
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported",
               file=sys.stderr)
         sys.exit(2)
     import torch

@@ -1,7 +1,7 @@
 """Golden vectors of the reference's QPU emulator, for pinning the oracle bit for bit.
 
-Imports the reference from /root/reference (in the development container only: nothing here
-runs on a GPU box, and only the vectors are committed), runs small kernels on its strict
+Imports the reference from /root/reference (run only where that checkout exists; nothing here
+is imported by the tests, and only the vectors are committed), runs small kernels on its strict
 emulator and writes their inputs and outputs to tests/golden/emulator/*.npz:
 
     python tests/golden/make_emulator_vectors.py

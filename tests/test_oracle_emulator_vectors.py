@@ -1,8 +1,8 @@
 """The oracle against the reference's own QPU emulator, bit for bit.
 
 tests/golden/emulator/*.npz hold inputs and outputs of the reference's strict emulator
-(written by tests/golden/make_emulator_vectors.py, which imports the reference in the
-development container): one-op math kernels over seeded and special values
+(written by tests/golden/make_emulator_vectors.py, which imports the reference where its
+checkout exists): one-op math kernels over seeded and special values
 (piton/backend/lower.py: exp/exp2 :2716-2797, division :633-764, rsqrt/sqrt :766-795, 2899-2939),
 softmax_kernel rows with +inf / all -inf / -inf / NaN rows and rows of 1000-1823 columns at
 BLOCK_SIZE 1024 / 2048 (examples/kernels.py:60-76), the

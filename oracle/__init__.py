@@ -20,7 +20,7 @@ attention against float64 plus the reference tests' known answers; layernorm aga
 the digits MLP against the reference's known accuracy on its committed model and data. And
 bit for bit against the reference's own emulator: golden vectors of exp, exp2, division, division
 by a uniform, 1/x, rsqrt, sqrt (seeded and special values), softmax rows (with +inf, all -inf,
--inf and NaN rows), the tutorial matmul, attention and the config-1 MLP, written by running the
+-inf and NaN rows), the tutorial matmul, attention and the digits MLP (He-normal weights, raw pixels), written by running the
 reference's emulator (tests/golden/emulator, tests/test_oracle_emulator_vectors.py).
 """
 from __future__ import annotations

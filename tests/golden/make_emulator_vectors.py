@@ -15,7 +15,7 @@ emulator and writes their inputs and outputs to tests/golden/emulator/*.npz:
   attention.npz attn_fwd_kernel (examples/attention.py:67-113) through run_attention
                 (examples/attention.py:200-222), causal and not
   mlp.npz       dense_layer_kernel (examples/nn_kernels.py:23-74) three times with the
-                launch of tests/test_nn_kernels.py:14-34, on config 1 (He-normal weights from
+                launch of tests/test_nn_kernels.py:14-34, on the digits MLP (He-normal weights from
                 seed 1729, raw 0..16 pixels) for the first 96 test images, every layer's output
   mlp_full.npz  the same chain's logits and predictions for all 1,797 test images
                 (`--full-mlp`, about half an hour of emulation)

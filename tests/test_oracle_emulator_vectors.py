@@ -7,7 +7,8 @@ checkout exists): one-op math kernels over seeded and special values
 softmax_kernel rows with +inf / all -inf / -inf / NaN rows and rows of 1000-1823 columns at
 BLOCK_SIZE 1024 / 2048 (examples/kernels.py:60-76), the
 tutorial matmul (examples/kernels.py:18-57), attention through run_attention
-(examples/attention.py:200-222) and three dense_layer_kernel launches on config 1, for 96 images and for all
+(examples/attention.py:200-222) and the digits MLP's three dense_layer_kernel launches (He-normal
+weights, raw [0, 16] pixels, 64 -> 128 -> 64 -> 10) for 96 images and for all
 1,797 (examples/nn_kernels.py:23-74). Every output must equal the oracle's bits (NaN equals NaN)."""
 import os
 
@@ -93,7 +94,7 @@ def test_attention(i):
     assert_bits(got, a[f"case{i}_o"])
 
 
-def test_config1_mlp_logits_and_predictions():
+def test_digits_mlp_logits_and_predictions():
     m = load("mlp")
     layers = digits.he_normal_mlp(seed=1729)
     chain = [(w, b, i < 2) for i, (w, b) in enumerate(layers)]
@@ -102,8 +103,8 @@ def test_config1_mlp_logits_and_predictions():
     np.testing.assert_array_equal(oracle.argmax_rows(logits, 10), m["pred"])
 
 
-def test_config1_mlp_all_1797_images():
-    """The emulator's three dense launches over every test image (config 1's whole batch)."""
+def test_digits_mlp_all_1797_images():
+    """The emulator's three dense launches over every one of the 1,797 test images."""
     m = load("mlp_full")
     x = np.load(os.path.join(os.path.dirname(__file__), "golden", "digits", "dataset.npz"))["test_images"]
     chain = [(w, b, i < 2) for i, (w, b) in enumerate(digits.he_normal_mlp(seed=1729))]

@@ -107,9 +107,22 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const float *x, float *
     int64_t c0 = 0;
     if (vec) {
         const int64_t n4 = n_cols / 4;
-        for (int64_t i = lane; i < n4; i += 64) {
+        auto fold = [&](const f32x4 &v) {
+            return MAX ? fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)) : (v.x + v.y) + (v.z + v.w);
+        };
+        int64_t i = lane;
+        // four 16-byte loads in flight per lane, folded in a fixed order
+        for (; i + 192 < n4; i += 256) {
+            const f32x4 *q = reinterpret_cast<const f32x4 *>(p) + i;
+            const f32x4 v0 = __builtin_nontemporal_load(q), v1 = __builtin_nontemporal_load(q + 64);
+            const f32x4 v2 = __builtin_nontemporal_load(q + 128), v3 = __builtin_nontemporal_load(q + 192);
+            const float f = MAX ? fmaxf(fmaxf(fold(v0), fold(v1)), fmaxf(fold(v2), fold(v3)))
+                                : (fold(v0) + fold(v1)) + (fold(v2) + fold(v3));
+            acc = MAX ? fmaxf(acc, f) : acc + f;
+        }
+        for (; i < n4; i += 64) {
             const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p) + i);
-            acc = MAX ? fmaxf(acc, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w))) : acc + ((v.x + v.y) + (v.z + v.w));
+            acc = MAX ? fmaxf(acc, fold(v)) : acc + fold(v);
         }
         c0 = 4 * n4;
     }

@@ -332,6 +332,16 @@ void gemm_f32_kernel(GemmArgs g) {
 // CU) measured the same; 32 is the default
 constexpr int DKT = PITON_GEMM_DIRECT_KT;
 constexpr int DKH = DKT / 2;               // k per lane half per tile
+#ifndef PITON_GEMM_DIRECT_MB
+#define PITON_GEMM_DIRECT_MB 2
+#endif
+#ifndef PITON_GEMM_DIRECT_NB
+#define PITON_GEMM_DIRECT_NB 2
+#endif
+// 32 x 32 blocks per wave: 2 x 2 at three waves per SIMD measured fastest (4096^3: 140.5
+// TFLOP/s; 4 x 2 and 2 x 4 at 292-296 VGPRs, one wave per SIMD: 137 and 134)
+constexpr int DMB = PITON_GEMM_DIRECT_MB, DNB = PITON_GEMM_DIRECT_NB;
+constexpr int DBM = 64 * DMB, DBN = 64 * DNB;                           // workgroup tile (2 x 2 waves)
 __global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(PITON_GEMM_DIRECT_WAVES)))
 void gemm_direct_kernel(GemmArgs g) {
     const int t = threadIdx.x;
@@ -339,8 +349,8 @@ void gemm_direct_kernel(GemmArgs g) {
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, l31 = lane & 31;
 
-    const int num_pid_m = (int)(g.M / GBM);
-    const int num_pid_n = (int)(g.N / GBN);
+    const int num_pid_m = (int)(g.M / DBM);
+    const int num_pid_n = (int)(g.N / DBN);
     const int pid = xcd_logical_id(blockIdx.x, gridDim.x, kXcdCount);
     const int in_group = g.group_m * num_pid_n;
     const int group_id = pid / in_group;
@@ -348,52 +358,52 @@ void gemm_direct_kernel(GemmArgs g) {
     const int gsize = min(num_pid_m - first_m, g.group_m);
     const int pid_m = first_m + (pid % in_group) % gsize;
     const int pid_n = (pid % in_group) / gsize;
-    const int64_t m0 = (int64_t)pid_m * GBM, n0 = (int64_t)pid_n * GBN;
+    const int64_t m0 = (int64_t)pid_m * DBM, n0 = (int64_t)pid_n * DBN;
 
     const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.a), (short)0,
                                                       (int)((g.M - 1) * g.s_am * 4 + g.K * 4), 0x00020000);
     const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.b), (short)0,
                                                       (int)((g.K - 1) * g.s_bk * 4 + g.N * 4), 0x00020000);
-    uint32_t va[2], vb[2];
+    uint32_t va[DMB], vb[DNB];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        va[i] = (uint32_t)(((m0 + wm * 64 + i * 32 + l31) * g.s_am + DKH * half) * 4);
-        vb[i] = (uint32_t)(((int64_t)(DKH * half) * g.s_bk + n0 + wn * 64 + i * 32 + l31) * 4);
-    }
+    for (int i = 0; i < DMB; i++) va[i] = (uint32_t)(((m0 + wm * 32 * DMB + i * 32 + l31) * g.s_am + DKH * half) * 4);
+#pragma unroll
+    for (int i = 0; i < DNB; i++)
+        vb[i] = (uint32_t)(((int64_t)(DKH * half) * g.s_bk + n0 + wn * 32 * DNB + i * 32 + l31) * 4);
     const uint32_t sbk4 = (uint32_t)(g.s_bk * 4);
 
     struct Ops {
-        f32x4 a[2][DKH / 4];
-        float b[2][DKH];
+        f32x4 a[DMB][DKH / 4];
+        float b[DNB][DKH];
     };
     auto load = [&](int kt, Ops &o) {
         const int ka = kt * (DKT * 4);
         const int kb = (int)((uint32_t)kt * DKT * sbk4);
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < DMB; i++)
 #pragma unroll
             for (int q = 0; q < DKH / 4; q++)
                 o.a[i][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(va[i] + 16 * q), ka, 0));
 #pragma unroll
         for (int s = 0; s < DKH; s++)
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < DNB; i++)
                 o.b[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)vb[i], kb + s * (int)sbk4, 0));
     };
-    f32x16 acc[2][2];
+    f32x16 acc[DMB][DNB];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < DMB; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < DNB; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
     auto mul = [&](const Ops &o) {
 #pragma unroll
         for (int s = 0; s < DKH; s++)
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < DMB; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int j = 0; j < DNB; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i][s >> 2][s & 3], o.b[j][s], acc[i][j], 0, 0, 0);
     };
     // K % (2 DKT) == 0: the tiles come in pairs. The last pair's prefetch loads the last tile
@@ -412,14 +422,14 @@ void gemm_direct_kernel(GemmArgs g) {
 
     // accumulator r of a 32x32 block holds row 8*(r/4) + 4*half + r%4, column l31
 #pragma unroll
-    for (int mb = 0; mb < 2; mb++)
+    for (int mb = 0; mb < DMB; mb++)
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) {
-            const int64_t col = n0 + wn * 64 + nb * 32 + l31;
+        for (int nb = 0; nb < DNB; nb++) {
+            const int64_t col = n0 + wn * 32 * DNB + nb * 32 + l31;
             const float bias = g.bias ? g.bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t row = m0 + wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                const int64_t row = m0 + wm * 32 * DMB + mb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                 float v = acc[mb][nb][r];
                 if (g.bias) v += bias;
                 if (g.relu && v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
@@ -615,9 +625,9 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
     const bool whole = al == VEC_ROW && bl == VEC_ROW && g.M % GBM == 0 && g.N % GBN == 0 && g.K % GBK == 0 && g.K > 0;
     // the direct kernel addresses rows by 32-bit byte offsets from the matrix base: positive row
     // strides and every element within 2^31 bytes
-    if (PITON_GEMM_DIRECT && whole && g.K % (2 * DKT) == 0 && g.s_am > 0 && g.s_bk > 0 &&
-        (g.M - 1) * g.s_am + g.K < (1LL << 29) && (g.K - 1) * g.s_bk + g.N < (1LL << 29))
-        hipLaunchKernelGGL(gemm_direct_kernel, dim3(nwg), dim3(GTHREADS), 0, st, g);
+    if (PITON_GEMM_DIRECT && whole && g.M % DBM == 0 && g.N % DBN == 0 && g.K % (2 * DKT) == 0 && g.s_am > 0 &&
+        g.s_bk > 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) && (g.K - 1) * g.s_bk + g.N < (1LL << 29))
+        hipLaunchKernelGGL(gemm_direct_kernel, dim3((unsigned)((g.M / DBM) * (g.N / DBN))), dim3(GTHREADS), 0, st, g);
     else if (whole)
         hipLaunchKernelGGL((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);
     else if (al == VEC_ROW) launch_b<VEC_ROW>(bl, g, nwg, st);

@@ -223,16 +223,10 @@ def bench_tinygpt():
                 graph=True)
 
 
-def cpu_baseline(a, b, budget_s=10.0):
-    """The oracle's matmul (round-toward-zero restatement, vectorised, all host threads up to
-    16) over row blocks of the same product, cycling through A's rows, until about budget_s
-    of work."""
-    import numpy as np
-
+def _oracle_rate(an, bn, threads, budget_s):
+    """Rows per second of the oracle's matmul on row blocks of A (cycling), about budget_s."""
     import oracle
-    an, bn = a.cpu().numpy(), b.cpu().numpy()
-    threads = max(1, min(16, os.cpu_count() or 1))
-    M, n, K = an.shape[0], bn.shape[1], bn.shape[0]
+    M = an.shape[0]
     rows, spent, total_rows, r0 = threads, 0.0, 0, 0
     while spent < budget_s:
         rows = min(rows, M - r0)
@@ -244,9 +238,43 @@ def cpu_baseline(a, b, budget_s=10.0):
         r0 = (r0 + rows) % M
         if dt < budget_s / 8:
             rows *= 2
-    flops = 2.0 * total_rows * n * K
-    return dict(value=flops / spent / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"{total_rows} rows of C = A B at {M}x{n}x{K}, cycling over A's rows ({spent:.1f} s)")
+    return total_rows, spent
+
+
+def cpu_baseline(a, b, budget_s=10.0, c_gpu=None):
+    """The oracle's matmul (round-toward-zero restatement, vectorised) over row blocks of the
+    same product, cycling through A's rows, with all host threads up to 16 for about budget_s
+    (the reported value), then with one thread and numpy's float64 matmul for a tenth of that
+    each. With c_gpu (the first rows of the GPU's C), the relative Frobenius error of the GPU
+    and of the oracle against float64 on those rows."""
+    import numpy as np
+
+    import oracle
+    from oracle import fp64
+    an, bn = a.cpu().numpy(), b.cpu().numpy()
+    threads = max(1, min(16, os.cpu_count() or 1))
+    M, n, K = an.shape[0], bn.shape[1], bn.shape[0]
+    total_rows, spent = _oracle_rate(an, bn, threads, budget_s)
+    flops_row = 2.0 * n * K
+    out = dict(value=total_rows * flops_row / spent / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+               sample=f"{total_rows} rows of C = A B at {M}x{n}x{K}, cycling over A's rows ({spent:.1f} s)")
+    rows1, spent1 = _oracle_rate(an, bn, 1, budget_s / 10)
+    out["value_1_thread"] = rows1 * flops_row / spent1 / 1e12
+    rows64, spent64, r0 = 0, 0.0, 0
+    while spent64 < budget_s / 10:
+        t0 = time.perf_counter()
+        np.matmul(an[r0:r0 + 64].astype(np.float64), bn.astype(np.float64))
+        spent64 += time.perf_counter() - t0
+        rows64 += 64
+        r0 = (r0 + 64) % max(1, M - 63)
+    out["numpy_fp64"] = dict(value=rows64 * flops_row / spent64 / 1e12, unit="TFLOP/s",
+                             threads=os.environ.get("OMP_NUM_THREADS", "numpy default"))
+    if c_gpu is not None:
+        rows = c_gpu.shape[0]
+        ref = fp64.matmul(an[:rows], bn)
+        out["err_vs_fp64"] = dict(rows=rows, gpu=fp64.rel_fro(np.asarray(c_gpu), ref),
+                                  oracle=fp64.rel_fro(np.asarray(oracle.matmul_fast(an[:rows], bn, threads=threads)), ref))
+    return out
 
 
 def main():
@@ -291,6 +319,7 @@ def main():
         "device": {k: info[k] for k in ("arch", "cu_count", "max_clock_khz", "hbm_bytes")},
     }
     a_host, b_host = (mm["a"].cpu(), mm["b"].cpu()) if not args.no_cpu else (None, None)
+    c_rows = mm["c"][:64].cpu().numpy() if not args.no_cpu else None
     del mm
     torch.cuda.empty_cache()
     if not args.no_extras:
@@ -299,7 +328,7 @@ def main():
         line["mlp"] = bench_mlp()
         line["tinygpt"] = bench_tinygpt()
     if not args.no_cpu:  # last: the GPU idles while the host cores work
-        line["cpu_baseline"] = cpu_baseline(a_host, b_host)
+        line["cpu_baseline"] = cpu_baseline(a_host, b_host, c_gpu=c_rows)
     print(json.dumps(line))
 
 

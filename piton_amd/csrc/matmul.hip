@@ -318,7 +318,7 @@ void gemm_f32_kernel(GemmArgs g) {
 // B operands 16 rows of its column (one 4-byte load per row, 128 contiguous bytes per
 // half-wave). Operands of tile k+1 are loaded while tile k multiplies (two register sets,
 // the loop unrolled by two). Buffer descriptors carry the matrices (each < 2 GiB); every load
-// lies inside them. 144 VGPRs:
+// lies inside them. 146 VGPRs:
 // three workgroups per CU. At 4096^3 this runs ~5 % faster than the LDS kernel, whose two
 // barriers per K tile left the matrix pipe idle 14 % of the time; at four workgroups per CU
 // (128 VGPRs) it spills and runs 10 % slower.
@@ -328,7 +328,7 @@ void gemm_f32_kernel(GemmArgs g) {
 #ifndef PITON_GEMM_DIRECT_WAVES
 #define PITON_GEMM_DIRECT_WAVES 3
 #endif
-// K per register tile: 32 (144 VGPRs, three workgroups per CU) and 16 (114 VGPRs, four per
+// K per register tile: 32 (146 VGPRs, three workgroups per CU) and 16 (114 VGPRs, four per
 // CU) measured the same; 32 is the default
 constexpr int DKT = PITON_GEMM_DIRECT_KT;
 constexpr int DKH = DKT / 2;               // k per lane half per tile

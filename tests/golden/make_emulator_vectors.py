@@ -19,6 +19,8 @@ emulator and writes their inputs and outputs to tests/golden/emulator/*.npz:
                 seed 1729, raw 0..16 pixels) for the first 96 test images, every layer's output
   mlp_full.npz  the same chain's logits and predictions for all 1,797 test images
                 (`--full-mlp`, about half an hour of emulation)
+  layernorm.npz row layernorm (the kernel of tests/test_reroll_reduce.py:199-208) at BLOCK 256
+                and 128, and add_kernel's x + y (`--layernorm`)
   softmax_long.npz  softmax_kernel rows at BLOCK_SIZE 1024 and 2048 (n_cols 1000, 1023, 1823),
                 which compile only with the reduction reroll of piton/reroll.py switched on
                 (PITON_REROLL_REDUCE=1, the build of tests/test_reroll_reduce.py:37-44)
@@ -81,6 +83,25 @@ def div_uniform_k(x_ptr, o_ptr, n, s, BLOCK: tl.constexpr):
     m = offs < n
     x = tl.load(x_ptr + offs, mask=m, other=1.0)
     tl.store(o_ptr + offs, x / s, mask=m)
+
+
+@piton.jit
+def rownorm_k(x_ptr, out_ptr, n, eps, BLOCK: tl.constexpr):
+    row = tl.program_id(0)
+    cols = tl.arange(0, BLOCK)
+    live = cols < n
+    v = tl.load(x_ptr + row * BLOCK + cols, mask=live, other=0.0)
+    mu = tl.sum(v, axis=0) / n
+    c = tl.where(live, v - mu, 0.0)
+    s2 = tl.sum(c * c, axis=0) / n
+    tl.store(out_ptr + row * BLOCK + cols, c / tl.sqrt(s2 + eps), mask=live)
+
+
+@piton.jit
+def add_k(x_ptr, y_ptr, o_ptr, n, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    m = offs < n
+    tl.store(o_ptr + offs, tl.load(x_ptr + offs, mask=m) + tl.load(y_ptr + offs, mask=m), mask=m)
 
 
 SPECIALS = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -1.0, 2.0, 0.5, 4.0, 9.0, 88.7, 88.73, -87.3,
@@ -232,12 +253,54 @@ def softmax_long_vectors(rng):
     return out
 
 
+def layernorm_vectors(rng):
+    """Row layernorm without affine (the kernel of tests/test_reroll_reduce.py:199-208) over 3 rows
+    at (BLOCK, n) = (256, 256), (256, 200), (128, 100), (128, 127), built the way that test builds
+    it (reduction reroll on; store slots 1 at BLOCK 256, 0 with a 360-instruction cache
+    threshold at 128), and add_kernel's x + y over seeded and special values."""
+    import piton.reroll as reroll
+    os.environ["PITON_REROLL_REDUCE"] = "1"
+    sig = {"x_ptr": "*fp32", "out_ptr": "*fp32", "n": "i32", "eps": "fp32"}
+    out, done, rows = {}, 0, 3
+    for block, n, slots in ((256, 256, "1"), (256, 200, "1"), (128, 100, "0"), (128, 127, "0")):
+        os.environ["PITON_STORE_SLOTS"] = slots
+        saved = reroll.ICACHE_INSTRUCTIONS
+        if block == 128:
+            reroll.ICACHE_INSTRUCTIONS = 360
+        try:
+            ck = pc.compile(rownorm_k, sig, {"BLOCK": block}, grid=(4,))
+        except Exception as e:  # a build the reference cannot make is recorded, not faked
+            print(f"layernorm BLOCK {block} n {n}: no build ({type(e).__name__}: {e})", flush=True)
+            continue
+        finally:
+            reroll.ICACHE_INSTRUCTIONS = saved
+        x = (rng.standard_normal((rows, block)) * 2 + 1).astype(np.float32)
+        y = np.full(rows * block, np.nan, np.float32)
+        run_emulator(ck, (rows,), {"x_ptr": x.ravel().copy(), "out_ptr": y, "n": n, "eps": 1e-5})
+        out[f"case{done}_x"], out[f"case{done}_y"] = x, y.reshape(rows, block)
+        out[f"case{done}_shape"] = np.array([rows, n, block], np.int64)
+        done += 1
+    out["n_cases"] = np.int64(done)
+    os.environ.pop("PITON_STORE_SLOTS", None)
+    xa = np.concatenate([(rng.standard_normal(1000) * 10).astype(np.float32), SPECIALS])
+    ya = np.concatenate([rng.standard_normal(1000).astype(np.float32), rng.permutation(SPECIALS)])
+    oa = np.zeros_like(xa)
+    add_k[(piton.cdiv(len(xa), 128),)](xa, ya, oa, len(xa), BLOCK=128)
+    out["add_x"], out["add_y"], out["add_out"] = xa, ya, oa
+    return out
+
+
 def main():
     os.makedirs(OUT, exist_ok=True)
     if "--softmax-long" in sys.argv:
         t0 = time.time()
         np.savez_compressed(os.path.join(OUT, "softmax_long.npz"), **softmax_long_vectors(np.random.default_rng(7)))
         print(f"softmax_long: {time.time() - t0:.1f} s", flush=True)
+        return
+    if "--layernorm" in sys.argv:
+        t0 = time.time()
+        np.savez_compressed(os.path.join(OUT, "layernorm.npz"), **layernorm_vectors(np.random.default_rng(11)))
+        print(f"layernorm: {time.time() - t0:.1f} s", flush=True)
         return
     if "--full-mlp" in sys.argv:
         t0 = time.time()

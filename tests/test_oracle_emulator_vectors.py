@@ -6,7 +6,8 @@ checkout exists): one-op math kernels over seeded and special values
 (piton/backend/lower.py: exp/exp2 :2716-2797, division :633-764, rsqrt/sqrt :766-795, 2899-2939),
 softmax_kernel rows with +inf / all -inf / -inf / NaN rows and rows of 1000-1823 columns at
 BLOCK_SIZE 1024 / 2048 (examples/kernels.py:60-76), the
-tutorial matmul (examples/kernels.py:18-57), attention through run_attention
+tutorial matmul (examples/kernels.py:18-57), row layernorm (tests/test_reroll_reduce.py:199-208) and
+add_kernel (examples/kernels.py:6-15), attention through run_attention
 (examples/attention.py:200-222) and the digits MLP's three dense_layer_kernel launches (He-normal
 weights, raw [0, 16] pixels, 64 -> 128 -> 64 -> 10) for 96 images and for all
 1,797 (examples/nn_kernels.py:23-74). Every output must equal the oracle's bits (NaN equals NaN)."""
@@ -79,6 +80,20 @@ def test_softmax_long_rows(i):
     s = load("softmax_long")
     rows, cols, block, _ = (int(v) for v in s[f"case{i}_shape"])
     assert_bits(np.asarray(oracle.softmax(s[f"case{i}_x"], cols, block)), s[f"case{i}_y"])
+
+
+@pytest.mark.parametrize("i", range(4))
+def test_layernorm_rows(i):
+    """The layernorm kernel of tests/test_reroll_reduce.py:199-208 at (BLOCK, n) = (256, 256),
+    (256, 200), (128, 100), (128, 127); columns past n stay as the emulator left them (NaN)."""
+    m = load("layernorm")
+    rows, n, block = (int(v) for v in m[f"case{i}_shape"])
+    assert_bits(oracle.layernorm(m[f"case{i}_x"], n, 1e-5, block), m[f"case{i}_y"])
+
+
+def test_add():
+    m = load("layernorm")
+    assert_bits(oracle.add(m["add_x"], m["add_y"]), m["add_out"])
 
 
 @pytest.mark.parametrize("i", range(2))

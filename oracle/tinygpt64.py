@@ -17,15 +17,18 @@ def layernorm(x, eps):
     return d / np.sqrt((d * d).mean(axis=-1, keepdims=True) + eps)
 
 
-def generate(weights: dict, prompts, steps: int, n_layers=4, n_heads=4, eps=1e-5):
+def generate(weights: dict, prompts, steps: int, n_layers=4, n_heads=4, eps=1e-5, score_scale=None,
+             activation=None):
     """Greedy decoding in float64 with a K/V cache. Returns (tokens [B, T0 + steps], margins
-    [B, steps]: the top-1 minus top-2 logit of every step)."""
+    [B, steps]: the top-1 minus top-2 logit of every step). score_scale (default 1/sqrt(d_head))
+    and activation (default ReLU) exist so that tests can plant a wrong one."""
     w = {k: np.asarray(v, np.float64) for k, v in weights.items()}
     prompts = np.asarray(prompts)
     B, T0 = prompts.shape
     D = w["tok"].shape[1]
     Dh = D // n_heads
-    scale = 1.0 / np.sqrt(Dh)
+    scale = 1.0 / np.sqrt(Dh) if score_scale is None else score_scale
+    act = (lambda z: np.maximum(z, 0.0)) if activation is None else activation
     total = T0 + steps
     tokens = np.zeros((B, total), np.int64)
     tokens[:, :T0] = prompts
@@ -54,7 +57,7 @@ def generate(weights: dict, prompts, steps: int, n_layers=4, n_heads=4, eps=1e-5
             a = (p @ vals).transpose(0, 2, 1, 3).reshape(B, T, D)
             x = x + a @ w[f"wo{i}"] + w[f"bo{i}"]
             h = layernorm(x, eps)
-            x = x + np.maximum(h @ w[f"w1{i}"] + w[f"b1{i}"], 0.0) @ w[f"w2{i}"] + w[f"b2{i}"]
+            x = x + act(h @ w[f"w1{i}"] + w[f"b1{i}"]) @ w[f"w2{i}"] + w[f"b2{i}"]
         return layernorm(x[:, -1], eps) @ w["lm"]
 
     logits = forward(0, T0)

@@ -381,10 +381,6 @@ __device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 #ifndef PITON_ATTN_PAIR_MODE
 #define PITON_ATTN_PAIR_MODE 2
 #endif
-// Q staging: Q requested before the first K/V block and unrolled (1), or after them (0)
-#ifndef PITON_ATTN_Q_FIRST
-#define PITON_ATTN_Q_FIRST 1
-#endif
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
@@ -455,11 +451,17 @@ template <int D, bool PAIR>
 __global__ __launch_bounds__(64 * ANW) __attribute__((amdgpu_waves_per_eu(PAIR ? 2 : PITON_ATTN_FAST_WAVES)))
 void attn_fwd_fast(AttnArgs g) {
     constexpr int NG = PAIR ? 2 : 1;
-    constexpr int SLAB_F = ANW * ABN * D, COMPUTE_F = SLAB_F + NG * D * AQG;
-    constexpr int STATE_F = ANW * (D / 2 + 2) * 64, MERGE_F = NG * STATE_F;  // every wave's (O, m, l) per group
-    __shared__ __attribute__((aligned(16))) float lds[COMPUTE_F > MERGE_F ? COMPUTE_F : MERGE_F];
-    float(*vslab)[ABN][D] = reinterpret_cast<float(*)[ABN][D]>(lds);
-    float(*qT)[D][AQG] = reinterpret_cast<float(*)[D][AQG]>(lds + SLAB_F);
+    // Two LDS objects. The V slabs (written by LDS-DMA) and the Q tiles are distinct variables,
+    // so the compiler's wait-count pass can tell the Q reads of a score product from the V
+    // copies in flight and does not make them wait for those copies. The merge reuses both: each
+    // wave's O rows in the first, its (m, l) in the second.
+    constexpr int SLAB_F = ANW * ABN * D, XO_F = NG * ANW * (D / 2) * 64;
+    constexpr int QT_F = NG * D * AQG, XM_F = NG * ANW * 2 * 64;
+    __shared__ __attribute__((aligned(16))) float lds_v[SLAB_F > XO_F ? SLAB_F : XO_F];
+    __shared__ __attribute__((aligned(16))) float lds_q[QT_F > XM_F ? QT_F : XM_F];
+    static_assert(!PAIR || sizeof(lds_v) + sizeof(lds_q) <= 80 * 1024, "two paired workgroups share a CU's 160 KB");
+    float(*vslab)[ABN][D] = reinterpret_cast<float(*)[ABN][D]>(lds_v);
+    float(*qT)[D][AQG] = reinterpret_cast<float(*)[D][AQG]>(lds_q);
 
     const int t = threadIdx.x, lane = t & 63, half = lane >> 5, l31 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -493,6 +495,8 @@ void attn_fwd_fast(AttnArgs g) {
     // byte offsets: K half row of key kb*32 + l31; V chunk c of block kb at v_lane + kb*v_blk + c*v_c
     constexpr int KPC = 64 / (D / 4);  // V keys per float4 chunk step of the lane
     constexpr int NVQ = ABN * D / 4 / 64;
+    constexpr int K_LOADS = D / 8;  // 16-byte loads of load_k: one lane-half row of the block
+    static_assert(K_LOADS <= 63 && NVQ <= 63, "loads per block within the vmcnt range");
     const uint32_t k_lane = ((uint32_t)l31 * s_kn + half * (D / 2)) * 4u, k_blk = (uint32_t)ABN * s_kn * 4u;
     const uint32_t v_lane = ((uint32_t)(lane / (D / 4)) * s_vn + 4 * (lane % (D / 4))) * 4u;
     const uint32_t v_blk = (uint32_t)ABN * s_vn * 4u, v_c = (uint32_t)KPC * s_vn * 4u;
@@ -529,7 +533,6 @@ void attn_fwd_fast(AttnArgs g) {
         dq = r % (D / 4);
     };
     float kf[D / 2];
-#if PITON_ATTN_Q_FIRST
     f32x4 qv[QIT];
 #pragma unroll
     for (int c = 0; c < QIT; c++) {
@@ -545,31 +548,14 @@ void attn_fwd_fast(AttnArgs g) {
 #pragma unroll
         for (int e = 0; e < 4; e++) qT[gi][4 * dq + e][j] = qv[c][e] * g.scale;
     }
-#else
-    if (n > 0) {  // the first block's K and V are in flight while Q is staged
-        load_k(kf, kb_of(0));
-        fetch_v(kb_of(0));
-    }
-    for (int c = 0; c < QIT; c++) {
-        int gi, j, dq;
-        q_chunk(c, gi, j, dq);
-        const f32x4 f = bload4(rq, ((uint32_t)((gi ? qg1 : qg0) * AQG + j) * s_qm + 4 * dq) * 4u);
-#pragma unroll
-        for (int e = 0; e < 4; e++) qT[gi][4 * dq + e][j] = f[e] * g.scale;
-    }
-#endif
-#if PITON_ATTN_Q_FIRST
     // the other waves need the Q tiles only: wait for this wave's LDS writes and meet at the
     // barrier, without the release fence of __syncthreads, whose wait covers every memory
     // operation in flight (the first block's K, which only this wave reads, included)
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(kWaitcntLgkm0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     __builtin_amdgcn_sched_barrier(0);
-#else
-    __syncthreads();
-#endif
 
     f32x16 o[D / 32], po[D / 32];  // the running state and (PAIR) the parked first group's
 #pragma unroll
@@ -579,15 +565,15 @@ void attn_fwd_fast(AttnArgs g) {
     float m_i = -INFINITY, l_i = 0.f, pm = -INFINITY, pl = 0.f;
 
     if (n > 0) {
-#if PITON_ATTN_Q_FIRST
-        // the first block's V after the start-up burst of Q and K (it is needed only after the
-        // first scores and exps), and before block 1's K, as the loop's waits assume
-        fetch_v(kb_of(0));
-#endif
         f32x16 st = block_scores_lds<D>(kf, qT[0], half, l31);
-        // the loop starts with the next block's K issued before this block's V is waited for,
-        // the order it keeps every iteration, so each wait on K lets newer V loads stay in flight
+        // Every pass of the loop starts with block j+1's K in flight ahead of block j's V, so
+        // the wait for that K lets the newer V copies stay in flight. Block 0's V is therefore
+        // requested after block 1's K: issued before it (as soon as Q is staged), the compiler
+        // merges the two orders at the loop head, assumes the V copies are the older loads in
+        // every pass and waits for them at the next block's score product.
         load_k(kf, kb_of(1));  // past the list it reads a block nobody uses (or zeros)
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_v(kb_of(0));
         __builtin_amdgcn_sched_barrier(0);
         auto step = [&](int j, auto has_next) {
             constexpr bool NEXT = decltype(has_next)::value;
@@ -598,16 +584,16 @@ void attn_fwd_fast(AttnArgs g) {
             if constexpr (NEXT) st_next = block_scores_lds<D>(kf, qT[PAIR && j + 1 >= n0 ? 1 : 0], half, l31);
             online_exp(st, mref, l_i);
             if constexpr (NEXT) load_k(kf, kb_of(j + 2));
-            // block j's V is in the slab once at most the 8 K loads just issued are in flight
-            // (vmcnt counts in issue order; the scheduling barriers keep that order)
+            // block j's V is in the slab once at most the K loads just issued (D / 8 of them) are
+            // in flight (vmcnt counts in issue order; the scheduling barriers keep that order)
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(NEXT ? 0x0F78 : 0x0F70);  // vmcnt(8) / vmcnt(0)
+            __builtin_amdgcn_s_waitcnt(NEXT ? waitcnt_vm(K_LOADS) : waitcnt_vm(0));
             __builtin_amdgcn_sched_barrier(0);
             wave_lds_sync();  // rows written for other lanes are visible to the operand reads
             block_pv<D>(o, st, vw, half, l31);
             if constexpr (NEXT) {
                 __builtin_amdgcn_sched_barrier(0);
-                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the operand reads have their data
+                __builtin_amdgcn_s_waitcnt(kWaitcntLgkm0);  // the operand reads have their data
                 __builtin_amdgcn_sched_barrier(0);
                 wave_lds_sync();
                 fetch_v(kb_of(j + 1));
@@ -633,10 +619,11 @@ void attn_fwd_fast(AttnArgs g) {
     }
 
     // merge: every wave's state of every group into LDS, then each wave a quarter of the rows
-    float(*xs)[STATE_F] = reinterpret_cast<float(*)[STATE_F]>(lds);
+    auto xo_of = [&](int gi) { return reinterpret_cast<float(*)[D / 2][64]>(lds_v + gi * ANW * (D / 2) * 64); };
+    auto xm_of = [&](int gi) { return reinterpret_cast<float(*)[2][64]>(lds_q + gi * ANW * 2 * 64); };
     auto put = [&](int gi, const f32x16 (&so)[D / 32], float sm, float sl) {
-        float(*xo)[D / 2][64] = reinterpret_cast<float(*)[D / 2][64]>(xs[gi]);
-        float(*xm)[2][64] = reinterpret_cast<float(*)[2][64]>(xs[gi] + ANW * (D / 2) * 64);
+        float(*xo)[D / 2][64] = xo_of(gi);
+        float(*xm)[2][64] = xm_of(gi);
 #pragma unroll
         for (int b = 0; b < D / 32; b++)
 #pragma unroll
@@ -645,7 +632,7 @@ void attn_fwd_fast(AttnArgs g) {
         xm[wave][1][lane] = sl;
     };
     // every V copy into the slabs has landed before the LDS is reused for the merge
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();  // every wave is done with its slab and the Q tiles
     const bool second = PAIR && n1 > 0;  // the running state is the second group's
     put(second ? 1 : 0, o, m_i, l_i);
@@ -653,8 +640,7 @@ void attn_fwd_fast(AttnArgs g) {
     __syncthreads();
     for (int gi = 0; gi < ng; gi++) {
         const int qi = (gi ? qg1 : qg0) * AQG + l31;
-        merge_quarter<D>(reinterpret_cast<const float(*)[D / 2][64]>(xs[gi]),
-                         reinterpret_cast<const float(*)[2][64]>(xs[gi] + ANW * (D / 2) * 64),
+        merge_quarter<D>(xo_of(gi), xm_of(gi),
                          g.o + bi * g.s_ob + h * g.s_oh + (int64_t)qi * g.s_om, qi < n_ctx);
     }
 }

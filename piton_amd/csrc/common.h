@@ -71,6 +71,12 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
     return op(op(a, b), op(c, d));
 }
 
+// s_waitcnt immediates (GFX9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+// waitcnt_vm(n): wait until at most n vector-memory operations are in flight, nothing else.
+constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+// wait until every LDS / scalar-memory operation has completed, nothing else
+constexpr int kWaitcntLgkm0 = 0xC07F;
+
 // Orders LDS traffic between the lanes of one wavefront: stores before the fence are visible
 // to loads after it in every lane of the wave. The hardware already runs a wave's LDS
 // operations in order; the fences stop the compiler from moving a load above a store that

@@ -618,6 +618,10 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
     if (g.M == 0 || g.N == 0) return PITON_OK;
     const int64_t tiles = ((g.M + GBM - 1) / GBM) * ((g.N + GBN - 1) / GBN);
     PITON_REQUIRE(tiles <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "%s: %lld tiles exceed one grid", what, (long long)tiles);
+    // a group taller than the tile rows orders tiles exactly as a group of all of them does;
+    // the clamp keeps group_m * num_pid_n within the tile count (no 32-bit overflow in the kernels)
+    const int64_t num_pid_m = (g.M + GBM - 1) / GBM;
+    if (g.group_m > num_pid_m) g.group_m = (int)num_pid_m;
     g.a_kfast = llabs(g.s_ak) <= llabs(g.s_am);
     g.b_nfast = llabs(g.s_bn) <= llabs(g.s_bk);
     const int al = layout_a(g), bl = layout_b(g);

@@ -146,8 +146,10 @@ def test_whole_tile_shapes_with_padded_rows(M, N, K, pad):
     assert (got[:, N:] == -7.0).all()
 
 
-@pytest.mark.parametrize("group", [1, 3, 8, 64])
+@pytest.mark.parametrize("group", [1, 3, 8, 64, 2 ** 31 - 1])
 def test_group_order_does_not_change_bits(group):
+    """Any GROUP_SIZE_M, up to the largest int32 (a group taller than the tile rows orders the
+    tiles as one group of all of them), gives the same bits."""
     g = torch.Generator(device="cuda").manual_seed(11)
     a = torch.rand((700, 500), device="cuda", generator=g)
     b = torch.rand((500, 900), device="cuda", generator=g)
@@ -156,7 +158,7 @@ def test_group_order_does_not_change_bits(group):
     assert torch.equal(base, other)
 
 
-@pytest.mark.parametrize("group", [1, 3, 64])
+@pytest.mark.parametrize("group", [1, 3, 64, 2 ** 31 - 1])
 def test_group_order_does_not_change_bits_whole_tiles(group):
     g = torch.Generator(device="cuda").manual_seed(12)
     a = torch.rand((640, 256), device="cuda", generator=g)

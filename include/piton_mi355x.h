@@ -51,6 +51,16 @@ typedef struct {
     char arch[64];             /* gcnArchName */
 } piton_device_info_t;
 
+/* One kernel launch made by the last entry call of this thread (piton_mi355x_last_launches). */
+typedef struct {
+    char kernel[96];           /* the device kernel as the library's source names it */
+    uint32_t grid[3];          /* workgroups */
+    uint32_t block[3];         /* work-items per workgroup */
+    uint32_t lds_bytes;        /* static + dynamic LDS per workgroup */
+    int32_t vgprs;             /* vector registers per lane (hipFuncGetAttributes numRegs) */
+    uint32_t scratch_bytes;    /* private memory per lane (register spills) */
+} piton_launch_info_t;
+
 /* Version of this ABI (PITON_MI355X_ABI_VERSION). No reference counterpart. */
 PITON_API int32_t piton_mi355x_abi_version(void);
 
@@ -60,6 +70,13 @@ PITON_API const char *piton_mi355x_last_error(void);
 /* Properties of the current device, used for roofline figures. No reference counterpart;
  * it plays the role of piton_qpu_count (pi/runtime/piton_rt.h:70). */
 PITON_API int32_t piton_mi355x_device_info(piton_device_info_t *out);
+
+/* The kernel launches (up to 8) of this thread's last entry call that reached the device:
+ * *count receives their number, and the first min(max, *count) are written to out (out may be
+ * NULL when max is 0). The counterpart of the emulator statistics the reference stores in
+ * CompiledKernel.last_stats after a launch (piton/runtime/launcher.py:238-245,
+ * piton/qpu/emulator.py:1111-1174): what ran, on how many workgroups, with what resources. */
+PITON_API int32_t piton_mi355x_last_launches(piton_launch_info_t *out, int32_t max, int32_t *count);
 
 /* matmul_kernel (examples/kernels.py:18-57): C[M,N] = A[M,K] B[K,N] in float32 through six
  * runtime element strides; rows/cols past M/N are never stored and the K tail adds nothing.

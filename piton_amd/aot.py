@@ -30,90 +30,15 @@ import inspect
 import os
 import sys
 
+from .runtime import table
+
 C_TYPES = {"*fp32": "float *", "*i32": "int32_t *", "*u32": "uint32_t *", "i32": "int32_t", "u32": "uint32_t",
            "fp32": "float", "i1": "int32_t"}
 
 
-def cdiv_c(a, b):
-    return f"((({a}) + ({b}) - 1) / ({b}))"
-
-
-# Per kernel: the library entry, its argument expressions in terms of the kernel's parameters
-# ({name}) and the launch grid (gx, gy, gz), and the canonical grid (None: any value, named by
-# that axis). The mapping is the one piton_amd.runtime.launcher's planners apply at run time.
-KERNELS = {
-    "matmul_kernel": dict(
-        params=("a_ptr", "b_ptr", "c_ptr", "M", "N", "K", "stride_am", "stride_ak", "stride_bk", "stride_bn",
-                "stride_cm", "stride_cn", "BLOCK_SIZE_M", "BLOCK_SIZE_N", "BLOCK_SIZE_K", "GROUP_SIZE_M"),
-        entry="piton_mi355x_matmul",
-        call=("{a_ptr}", "{b_ptr}", "{c_ptr}", "{M}", "{N}", "{K}", "{stride_am}", "{stride_ak}", "{stride_bk}",
-              "{stride_bn}", "{stride_cm}", "{stride_cn}", "{GROUP_SIZE_M}"),
-        grid=(cdiv_c("{M}", "{BLOCK_SIZE_M}") + " * " + cdiv_c("{N}", "{BLOCK_SIZE_N}"), "1", "1")),
-    "softmax_kernel": dict(
-        params=("output_ptr", "input_ptr", "input_row_stride", "output_row_stride", "n_cols", "BLOCK_SIZE"),
-        entry="piton_mi355x_softmax",
-        call=("{output_ptr}", "{input_ptr}", "{input_row_stride}", "{output_row_stride}", "{n_cols}", "gx",
-              "{BLOCK_SIZE}"),
-        grid=(None, "1", "1")),
-    "attn_fwd_kernel": dict(
-        params=("Q", "K", "V", "Out", "sm_scale", "stride_qh", "stride_qm", "stride_kh", "stride_kn", "stride_kk",
-                "stride_vh", "stride_vn", "stride_oh", "stride_om", "N_CTX", "HEAD_DIM", "BLOCK_M", "BLOCK_N",
-                "CAUSAL", "EVEN_N"),
-        entry="piton_mi355x_attn_fwd",
-        call=("{Q}", "{K}", "{V}", "{Out}", "{sm_scale}", "{stride_qh}", "{stride_qm}", "{stride_kh}",
-              "{stride_kn}", "{stride_kk}", "{stride_vh}", "{stride_vn}", "{stride_oh}", "{stride_om}", "{N_CTX}",
-              "gy", "{HEAD_DIM}", "{CAUSAL}"),
-        grid=(cdiv_c("{N_CTX}", "{BLOCK_M}"), None, "1"),
-        check="!({EVEN_N}) || ({N_CTX}) % ({BLOCK_N}) == 0"),
-    "dense_layer_kernel": dict(
-        params=("x_ptr", "w_ptr", "bias_ptr", "y_ptr", "M", "N", "K", "BLOCK_SIZE_M", "BLOCK_SIZE_N",
-                "BLOCK_SIZE_K", "GROUP_SIZE_M", "ADD_BIAS", "RELU"),
-        entry="piton_mi355x_dense",
-        call=("{x_ptr}", "{w_ptr}", "({ADD_BIAS}) ? {bias_ptr} : (const float *)0", "{y_ptr}", "{M}", "{N}", "{K}",
-              "{ADD_BIAS}", "{RELU}", "(int32_t *)0", "0"),
-        grid=(cdiv_c("{M}", "{BLOCK_SIZE_M}") + " * " + cdiv_c("{N}", "{BLOCK_SIZE_N}"), "1", "1")),
-    "add_kernel": dict(
-        params=("x_ptr", "y_ptr", "output_ptr", "n_elements", "BLOCK_SIZE"),
-        entry="piton_mi355x_add",
-        call=("{x_ptr}", "{y_ptr}", "{output_ptr}", "{n_elements}"),
-        grid=(cdiv_c("{n_elements}", "{BLOCK_SIZE}"), "1", "1")),
-    "layernorm_kernel": dict(
-        params=("x_ptr", "out_ptr", "n", "eps", "BLOCK"),
-        entry="piton_mi355x_layernorm",
-        call=("{x_ptr}", "{out_ptr}", "(({n}) < ({BLOCK}) ? ({n}) : ({BLOCK}))", "{eps}", "gx", "{BLOCK}"),
-        grid=(None, "1", "1")),
-}
-
-
-def _map_spec(entry, ptrs, scalars=()):
-    return dict(params=(*ptrs, "n", *scalars, "BLOCK") if "OP" not in scalars else (*ptrs, "n", "OP", "BLOCK"),
-                entry=entry, call=(*[f"{{{p}}}" for p in ptrs], "{n}", *[f"{{{s}}}" for s in scalars]),
-                grid=(cdiv_c("{n}", "{BLOCK}"), "1", "1"))
-
-
-def _row_spec(entry):
-    return dict(params=("x_ptr", "out_ptr", "n_cols", "stride", "BLOCK_M", "BLOCK_N"), entry=entry,
-                call=("{x_ptr}", "{out_ptr}", "(long long)gx * ({BLOCK_M})",
-                      cdiv_c("{n_cols}", "{BLOCK_N}") + " * ({BLOCK_N})", "{stride}"),
-                grid=(None, "1", "1"))
-
-
-KERNELS.update({
-    "copy_kernel": _map_spec("piton_mi355x_copy", ("x_ptr", "out_ptr")),
-    "mul_kernel": _map_spec("piton_mi355x_mul", ("x_ptr", "y_ptr", "out_ptr")),
-    "fma_kernel": _map_spec("piton_mi355x_fma", ("x_ptr", "y_ptr", "out_ptr"), ("alpha",)),
-    "scaled_relu_kernel": _map_spec("piton_mi355x_scaled_relu", ("x_ptr", "out_ptr"), ("alpha",)),
-    "sfu_kernel": _map_spec("piton_mi355x_sfu", ("x_ptr", "out_ptr"), ("OP",)),
-    "log_kernel": _map_spec("piton_mi355x_log", ("x_ptr", "out_ptr")),
-    "idiv_kernel": _map_spec("piton_mi355x_idiv", ("x_ptr", "y_ptr", "q_ptr", "r_ptr")),
-    "row_sum_kernel": _row_spec("piton_mi355x_row_sum"),
-    "row_max_kernel": _row_spec("piton_mi355x_row_max"),
-    "transpose_kernel": dict(
-        params=("x_ptr", "out_ptr", "n_rows", "n_cols", "stride_x", "stride_out", "BLOCK_M", "BLOCK_N"),
-        entry="piton_mi355x_transpose",
-        call=("{x_ptr}", "{out_ptr}", "{n_rows}", "{n_cols}", "{stride_x}", "{stride_out}"),
-        grid=(cdiv_c("{n_rows}", "{BLOCK_M}") + " * " + cdiv_c("{n_cols}", "{BLOCK_N}"), "1", "1")),
-})
+# The kernel -> entry mapping is piton_amd.runtime.table's, the one the launcher evaluates at run
+# time; here its expressions are rendered as C.
+KERNELS = table.KERNELS
 
 
 def _parse_kv(text: str) -> dict:
@@ -175,9 +100,9 @@ def emit_c(kernel_name: str, params: tuple, signature: dict, constants: dict, ou
     spec = KERNELS.get(kernel_name)
     if spec is None:
         raise NotImplementedError(f"no mi355x kernel for {kernel_name!r}; this backend provides {sorted(KERNELS)}")
-    if tuple(params) != spec["params"]:
+    if tuple(params) != spec.params:
         raise NotImplementedError(f"{kernel_name}{tuple(params)} does not match the mi355x kernel's parameters "
-                                  f"{spec['params']}")
+                                  f"{spec.params}")
     both = set(signature) & set(constants)
     if both:
         raise ValueError(f"{sorted(both)} given both as runtime arguments and constants")
@@ -188,12 +113,8 @@ def emit_c(kernel_name: str, params: tuple, signature: dict, constants: dict, ou
         if t not in C_TYPES:
             raise TypeError(f"{n}: unsupported type {t!r} (one of {sorted(C_TYPES)})")
 
-    def sub(expr: str) -> str:
-        out = expr
-        for p in params:
-            val = f"args->{p}" if p in signature else _literal(constants[p])
-            out = out.replace("{" + p + "}", val)
-        return out
+    def sub(p: str) -> str:
+        return f"args->{p}" if p in signature else _literal(constants[p])
 
     sym = out_name
     guard = f"{sym.upper()}_H"
@@ -219,21 +140,18 @@ def emit_c(kernel_name: str, params: tuple, signature: dict, constants: dict, ou
           "uint32_t *usec);", "",
           "#ifdef __cplusplus", "}", "#endif", "", "#endif", ""]
 
-    gchecks = []
-    for axis, g in zip("xyz", spec["grid"]):
-        if g is not None:
-            gchecks.append(f"(long long)g{axis} != (long long)({sub(g)})")
+    gchecks = [f"(long long)g{axis} != (long long){g.c(sub)}" for axis, g in zip("xyz", spec.grid) if g is not None]
     c = [f'#include "{sym}.h"', "", "#include <hip/hip_runtime_api.h>", "", '#include "piton_mi355x.h"', "",
          f"int32_t {sym}_launch(const {sym}_args_t *args, unsigned gx, unsigned gy, unsigned gz, void *stream) {{",
          "    (void)args;"]
     if gchecks:
         c.append(f"    if ({' || '.join(gchecks)}) return PITON_EINVAL;")
-    else:
-        c.append("    (void)gy; (void)gz;")
-    if "check" in spec:
-        c.append(f"    if (!({sub(spec['check'])})) return PITON_EINVAL;")
-    call = ", ".join(sub(a) for a in spec["call"])
-    c += [f"    return {spec['entry']}({call}, stream);", "}", "",
+    if len(gchecks) < 3:
+        c.append("    (void)gx; (void)gy; (void)gz;")
+    for cond, _msg in spec.checks:
+        c.append(f"    if (!{cond.c(sub)}) return PITON_EINVAL;")
+    call = ", ".join(e.c(sub) for e in spec.call)
+    c += [f"    return piton_mi355x_{spec.entry}({call}, stream);", "}", "",
           f"int32_t {sym}_launch_us(const {sym}_args_t *args, unsigned gx, unsigned gy, unsigned gz, "
           "uint32_t *usec) {",
           "    hipEvent_t e0, e1;",

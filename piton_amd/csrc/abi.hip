@@ -20,6 +20,23 @@ int set_error(int code, const char *fmt, ...) {
 
 void clear_error() { g_msg[0] = '\0'; }
 
+struct LaunchNote {
+    const void *fn;
+    const char *name;
+    dim3 grid, block;
+    uint32_t dyn_lds;
+};
+constexpr int kMaxNotes = 8;
+static thread_local LaunchNote g_notes[kMaxNotes];
+static thread_local int g_note_count = 0;
+
+void note_launch(const void *fn, const char *name, dim3 grid, dim3 block, uint32_t dyn_lds) {
+    if (g_note_count < kMaxNotes) g_notes[g_note_count] = LaunchNote{fn, name, grid, block, dyn_lds};
+    g_note_count++;
+}
+
+void reset_launches() { g_note_count = 0; }
+
 static thread_local int g_cu_count = 0;
 
 int device_cu_count() { return g_cu_count; }
@@ -28,6 +45,7 @@ int require_device() {
     // the architecture check is cached per thread and device: later calls cost one
     // hipGetDevice
     static thread_local int checked_dev = -1;
+    reset_launches();
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess && dev == checked_dev) return PITON_OK;
@@ -81,6 +99,51 @@ int32_t piton_mi355x_device_info(piton_device_info_t *out) {
     out->wavefront_size = p.warpSize;
     out->xcd_count = kXcdCount;
     strncpy(out->arch, p.gcnArchName, sizeof out->arch - 1);
+    clear_error();
+    return PITON_OK;
+}
+
+int32_t piton_mi355x_last_launches(piton_launch_info_t *out, int32_t max, int32_t *count) {
+    using namespace piton;
+    PITON_REQUIRE(count != nullptr && max >= 0 && (max == 0 || out != nullptr), PITON_EINVAL,
+                  "last_launches: null output or negative max");
+    const int n = g_note_count < kMaxNotes ? g_note_count : kMaxNotes;
+    *count = g_note_count;
+    for (int i = 0; i < n && i < max; i++) {
+        const LaunchNote &note = g_notes[i];
+        piton_launch_info_t &o = out[i];
+        memset(&o, 0, sizeof o);
+        // the source spelling, without the parentheses a template kernel is launched in
+        const char *nm = note.name;
+        size_t len = strlen(nm);
+        if (len >= 2 && nm[0] == '(' && nm[len - 1] == ')') {
+            nm++;
+            len -= 2;
+        }
+        if (len > sizeof o.kernel - 1) len = sizeof o.kernel - 1;
+        memcpy(o.kernel, nm, len);
+        o.grid[0] = note.grid.x, o.grid[1] = note.grid.y, o.grid[2] = note.grid.z;
+        o.block[0] = note.block.x, o.block[1] = note.block.y, o.block[2] = note.block.z;
+        // a kernel's attributes do not change: looked up once per kernel and thread
+        static thread_local const void *cached_fn[32];
+        static thread_local hipFuncAttributes cached_attr[32];
+        static thread_local int n_cached = 0;
+        int slot = -1;
+        for (int c = 0; c < n_cached; c++)
+            if (cached_fn[c] == note.fn) slot = c;
+        if (slot < 0) {
+            hipFuncAttributes attr;
+            if (hipFuncGetAttributes(&attr, note.fn) != hipSuccess)
+                return set_error(PITON_EHIP, "last_launches: hipFuncGetAttributes failed for %s", o.kernel);
+            slot = n_cached < 32 ? n_cached++ : 31;
+            cached_fn[slot] = note.fn;
+            cached_attr[slot] = attr;
+        }
+        const hipFuncAttributes &attr = cached_attr[slot];
+        o.lds_bytes = (uint32_t)attr.sharedSizeBytes + note.dyn_lds;
+        o.vgprs = attr.numRegs;
+        o.scratch_bytes = (uint32_t)attr.localSizeBytes;
+    }
     clear_error();
     return PITON_OK;
 }

@@ -647,8 +647,8 @@ void attn_fwd_fast(AttnArgs g) {
 
 template <int D>
 static void launch_d(int kl, const AttnArgs &g, dim3 grid, hipStream_t st) {
-    if (kl == K_VEC_D) hipLaunchKernelGGL((attn_fwd_kernel_f32<D, K_VEC_D>), grid, dim3(64 * ANW), 0, st, g);
-    else hipLaunchKernelGGL((attn_fwd_kernel_f32<D, K_SCALAR>), grid, dim3(64 * ANW), 0, st, g);
+    if (kl == K_VEC_D) PITON_LAUNCH((attn_fwd_kernel_f32<D, K_VEC_D>), grid, dim3(64 * ANW), 0, st, g);
+    else PITON_LAUNCH((attn_fwd_kernel_f32<D, K_SCALAR>), grid, dim3(64 * ANW), 0, st, g);
 }
 
 // One new query per (batch, head) against keys 0 .. n_keys-1 of a cache (the decode step of a
@@ -874,11 +874,11 @@ static int attn_launch(AttnArgs g, int64_t batch, int64_t n_heads, int32_t head_
         if (pair) grid = dim3((unsigned)pairs);
     }
     if (fast && head_dim == 64) {
-        if (pair) hipLaunchKernelGGL((attn_fwd_fast<64, true>), grid, dim3(64 * ANW), 0, st, g);
-        else hipLaunchKernelGGL((attn_fwd_fast<64, false>), grid, dim3(64 * ANW), 0, st, g);
+        if (pair) PITON_LAUNCH((attn_fwd_fast<64, true>), grid, dim3(64 * ANW), 0, st, g);
+        else PITON_LAUNCH((attn_fwd_fast<64, false>), grid, dim3(64 * ANW), 0, st, g);
     } else if (fast) {
-        if (pair) hipLaunchKernelGGL((attn_fwd_fast<32, true>), grid, dim3(64 * ANW), 0, st, g);
-        else hipLaunchKernelGGL((attn_fwd_fast<32, false>), grid, dim3(64 * ANW), 0, st, g);
+        if (pair) PITON_LAUNCH((attn_fwd_fast<32, true>), grid, dim3(64 * ANW), 0, st, g);
+        else PITON_LAUNCH((attn_fwd_fast<32, false>), grid, dim3(64 * ANW), 0, st, g);
     }
     else if (head_dim <= 32) launch_d<32>(kl, g, grid, st);
     else if (head_dim == 64) launch_d<64>(kl, g, grid, st);
@@ -967,8 +967,8 @@ int32_t piton_mi355x_attn_decode(const float *q, const float *k, const float *v,
     const bool vec = aligned16(k) && stride_kn % 4 == 0 && stride_kh % 4 == 0 && stride_kb % 4 == 0;
 #define PITON_DEC(KERNEL, D)                                                                                        \
     do {                                                                                                            \
-        if (vec) hipLaunchKernelGGL((KERNEL<D, true>), grid, block, 0, st, g);                                      \
-        else hipLaunchKernelGGL((KERNEL<D, false>), grid, block, 0, st, g);                                         \
+        if (vec) PITON_LAUNCH((KERNEL<D, true>), grid, block, 0, st, g);                                      \
+        else PITON_LAUNCH((KERNEL<D, false>), grid, block, 0, st, g);                                         \
     } while (0)
     // short caches: every V offset the kernel forms (up to 256 rows and 64 dims) within 31 bits
     const bool short_cache = PITON_DECODE_SHORT && n_keys <= kShortDecodeKeys && stride_vn >= 0 &&

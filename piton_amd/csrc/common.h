@@ -25,6 +25,18 @@ int device_cu_count();
 // Turns the last launch's status into PITON_OK or PITON_EHIP naming `what`.
 int check_launch(const char *what);
 
+// Launch notes for piton_mi355x_last_launches: every kernel launch goes through PITON_LAUNCH,
+// which records the kernel, its grid, block and dynamic LDS in this thread's list (cleared by
+// require_device(), which every entry calls before its first launch).
+void note_launch(const void *fn, const char *name, dim3 grid, dim3 block, uint32_t dyn_lds);
+void reset_launches();
+#define PITON_LAUNCH(kernel, grid, block, lds, stream, ...)                                                   \
+    do {                                                                                                      \
+        ::piton::note_launch(reinterpret_cast<const void *>(&kernel), #kernel, dim3(grid), dim3(block),       \
+                             (uint32_t)(lds));                                                                \
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                                   \
+    } while (0)
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 

@@ -111,11 +111,11 @@ int32_t piton_mi355x_add(const float *x, const float *y, float *out, int64_t n, 
     int64_t done = 0;
     if (aligned16(x) && aligned16(y) && aligned16(out) && n >= 4) {
         const int64_t n4 = n / 4;
-        hipLaunchKernelGGL(add_vec4_kernel, dim3(grid_for(n4)), dim3(256), 0, st, reinterpret_cast<const f32x4 *>(x),
+        PITON_LAUNCH(add_vec4_kernel, dim3(grid_for(n4)), dim3(256), 0, st, reinterpret_cast<const f32x4 *>(x),
                            reinterpret_cast<const f32x4 *>(y), reinterpret_cast<f32x4 *>(out), n4);
         done = n4 * 4;
     }
-    if (done < n) hipLaunchKernelGGL(add_scalar_kernel, dim3(grid_for(n - done)), dim3(256), 0, st, x, y, out, done, n);
+    if (done < n) PITON_LAUNCH(add_scalar_kernel, dim3(grid_for(n - done)), dim3(256), 0, st, x, y, out, done, n);
     rc = check_launch("add");
     if (rc == PITON_OK) clear_error();
     return rc;
@@ -137,12 +137,12 @@ int32_t piton_mi355x_layernorm(const float *x, float *out, int64_t n, float eps,
     if (rows == 0) return PITON_OK;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-    if (per_lane <= 1) hipLaunchKernelGGL(layernorm_rows_kernel<1>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
-    else if (per_lane <= 2) hipLaunchKernelGGL(layernorm_rows_kernel<2>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
-    else if (per_lane <= 4) hipLaunchKernelGGL(layernorm_rows_kernel<4>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
-    else if (per_lane <= 8) hipLaunchKernelGGL(layernorm_rows_kernel<8>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
-    else if (per_lane <= 16) hipLaunchKernelGGL(layernorm_rows_kernel<16>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
-    else hipLaunchKernelGGL(layernorm_rows_kernel<32>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
+    if (per_lane <= 1) PITON_LAUNCH(layernorm_rows_kernel<1>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
+    else if (per_lane <= 2) PITON_LAUNCH(layernorm_rows_kernel<2>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
+    else if (per_lane <= 4) PITON_LAUNCH(layernorm_rows_kernel<4>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
+    else if (per_lane <= 8) PITON_LAUNCH(layernorm_rows_kernel<8>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
+    else if (per_lane <= 16) PITON_LAUNCH(layernorm_rows_kernel<16>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
+    else PITON_LAUNCH(layernorm_rows_kernel<32>, grid, block, 0, st, x, out, n, eps, rows, row_stride);
     rc = check_launch("layernorm");
     if (rc == PITON_OK) clear_error();
     return rc;
@@ -160,7 +160,7 @@ int32_t piton_mi355x_embedding(const int32_t *ids, int64_t ids_sb, int64_t ids_s
     if (rc) return rc;
     const int64_t total = batch * T * d_model;
     if (total == 0) return PITON_OK;
-    hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, ids, ids_sb, ids_st,
+    PITON_LAUNCH(embedding_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, ids, ids_sb, ids_st,
                        tok, pos, out, out_sb, out_st, T, d_model, vocab, pos_offset, total, err_flag);
     rc = check_launch("embedding");
     if (rc == PITON_OK) clear_error();

@@ -609,9 +609,9 @@ static int layout_b(const GemmArgs &g) {
 
 template <int A_L>
 static void launch_b(int bl, const GemmArgs &g, int nwg, hipStream_t st) {
-    if (bl == VEC_ROW) hipLaunchKernelGGL((gemm_f32_kernel<A_L, VEC_ROW, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
-    else if (bl == VEC_COL) hipLaunchKernelGGL((gemm_f32_kernel<A_L, VEC_COL, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
-    else hipLaunchKernelGGL((gemm_f32_kernel<A_L, SCALAR, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
+    if (bl == VEC_ROW) PITON_LAUNCH((gemm_f32_kernel<A_L, VEC_ROW, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
+    else if (bl == VEC_COL) PITON_LAUNCH((gemm_f32_kernel<A_L, VEC_COL, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
+    else PITON_LAUNCH((gemm_f32_kernel<A_L, SCALAR, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
 }
 
 static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
@@ -631,9 +631,9 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
     // strides and every element within 2^31 bytes
     if (PITON_GEMM_DIRECT && whole && g.M % DBM == 0 && g.N % DBN == 0 && g.K % (2 * DKT) == 0 && g.s_am > 0 &&
         g.s_bk > 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) && (g.K - 1) * g.s_bk + g.N < (1LL << 29))
-        hipLaunchKernelGGL(gemm_direct_kernel, dim3((unsigned)((g.M / DBM) * (g.N / DBN))), dim3(GTHREADS), 0, st, g);
+        PITON_LAUNCH(gemm_direct_kernel, dim3((unsigned)((g.M / DBM) * (g.N / DBN))), dim3(GTHREADS), 0, st, g);
     else if (whole)
-        hipLaunchKernelGGL((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);
+        PITON_LAUNCH((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);
     else if (al == VEC_ROW) launch_b<VEC_ROW>(bl, g, nwg, st);
     else if (al == VEC_COL) launch_b<VEC_COL>(bl, g, nwg, st);
     else launch_b<SCALAR>(bl, g, nwg, st);
@@ -683,7 +683,7 @@ int32_t piton_mi355x_dense(const float *x, const float *w, const float *bias, fl
     if (rc) return rc;
     if (argmax_out && M > 0) {
         PITON_REQUIRE((M + 3) / 4 <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "dense: M=%lld too large", (long long)M);
-        hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, y, M, N, n_classes,
+        PITON_LAUNCH(argmax_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, y, M, N, n_classes,
                            argmax_out);
         rc = check_launch("dense argmax");
         if (rc) return rc;
@@ -711,9 +711,9 @@ int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *w, const f
         PITON_REQUIRE((N + SMN - 1) / SMN <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "linear: N=%lld too large", (long long)N);
         const dim3 grid((unsigned)((N + SMN - 1) / SMN), (unsigned)((M + 15) / 16)), block(64 * SMWAVES);
         if (K % (16 * SMWAVES) == 0 && ldx % 4 == 0 && aligned16(x))
-            hipLaunchKernelGGL((gemm_small_m_kernel<true, false>), grid, block, 0, (hipStream_t)stream, g);
+            PITON_LAUNCH((gemm_small_m_kernel<true, false>), grid, block, 0, (hipStream_t)stream, g);
         else
-            hipLaunchKernelGGL((gemm_small_m_kernel<false, false>), grid, block, 0, (hipStream_t)stream, g);
+            PITON_LAUNCH((gemm_small_m_kernel<false, false>), grid, block, 0, (hipStream_t)stream, g);
         rc = check_launch("linear");
     } else {
         rc = launch_gemm(g, (hipStream_t)stream, "linear");
@@ -743,7 +743,7 @@ int32_t piton_mi355x_linear_ln(const float *x, int64_t ldx, float eps, const flo
     if (M == 0) return PITON_OK;
     GemmArgs g{x, w, y, M, N, K, ldx, 1, N, 1, ldy, 1, 1, bias, relu ? 1 : 0, residual, ldr, 0, 0, eps};
     const dim3 grid((unsigned)((N + SMN - 1) / SMN), (unsigned)((M + 15) / 16)), block(64 * SMWAVES);
-    hipLaunchKernelGGL((gemm_small_m_kernel<true, true>), grid, block, 0, (hipStream_t)stream, g);
+    PITON_LAUNCH((gemm_small_m_kernel<true, true>), grid, block, 0, (hipStream_t)stream, g);
     rc = check_launch("linear_ln");
     if (rc == PITON_OK) clear_error();
     return rc;
@@ -758,7 +758,7 @@ int32_t piton_mi355x_argmax_rows(const float *x, int64_t rows, int64_t ld, int64
     if (rc) return rc;
     if (rows == 0) return PITON_OK;
     PITON_REQUIRE(n <= 0x7FFFFFFF && (rows + 3) / 4 <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "argmax_rows: too large");
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, x,
+    PITON_LAUNCH(argmax_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, x,
                        rows, ld, (int)n, out);
     rc = check_launch("argmax_rows");
     if (rc == PITON_OK) clear_error();

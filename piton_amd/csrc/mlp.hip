@@ -117,7 +117,7 @@ extern "C" int32_t piton_mi355x_mlp3(const float *x, int64_t M, const float *w1,
     if (M == 0) return PITON_OK;
     const int64_t wgs = (M + MLP_ROWS - 1) / MLP_ROWS;
     PITON_REQUIRE(wgs <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "mlp3: M=%lld too large", (long long)M);
-    hipLaunchKernelGGL(mlp3_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, x, M, w1, b1, w2, b2, w3,
+    PITON_LAUNCH(mlp3_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, x, M, w1, b1, w2, b2, w3,
                        b3, (int)k0, (int)n1, (int)n2, (int)n3, logits, pred, n_classes);
     rc = check_launch("mlp3");
     if (rc == PITON_OK) clear_error();

@@ -63,11 +63,11 @@ static int launch_map(const float *x, const float *y, float *out, int64_t n, flo
     PITON_REQUIRE((n4 + 255) / 256 <= 0x7FFFFFFF && (n - 4 * n4 + 255) / 256 <= 0x7FFFFFFF, PITON_EUNSUPPORTED,
                   "%s: n=%lld too large", what, (long long)n);
     if (n4 > 0)
-        hipLaunchKernelGGL((map_vec4_kernel<Op, TWO>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+        PITON_LAUNCH((map_vec4_kernel<Op, TWO>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
                            reinterpret_cast<const f32x4 *>(x), reinterpret_cast<const f32x4 *>(y),
                            reinterpret_cast<f32x4 *>(out), n4, alpha);
     if (4 * n4 < n)
-        hipLaunchKernelGGL((map_scalar_kernel<Op, TWO>), dim3((unsigned)((n - 4 * n4 + 255) / 256)), dim3(256), 0,
+        PITON_LAUNCH((map_scalar_kernel<Op, TWO>), dim3((unsigned)((n - 4 * n4 + 255) / 256)), dim3(256), 0,
                            st, x, y, out, 4 * n4, n, alpha);
     return check_launch(what);
 }
@@ -271,10 +271,10 @@ int32_t piton_mi355x_idiv(const int32_t *x, const int32_t *y, int32_t *q, int32_
     const bool vec = aligned16(x) && aligned16(y) && aligned16(q) && aligned16(r);
     const int64_t n4 = vec ? n / 4 : 0;
     if (n4 > 0)
-        hipLaunchKernelGGL(idiv_kernel<true>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, x, y, q, r,
+        PITON_LAUNCH(idiv_kernel<true>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, x, y, q, r,
                            (int64_t)0, n4);
     if (4 * n4 < n)
-        hipLaunchKernelGGL(idiv_kernel<false>, dim3((unsigned)((n - 4 * n4 + 255) / 256)), dim3(256), 0, st, x, y,
+        PITON_LAUNCH(idiv_kernel<false>, dim3((unsigned)((n - 4 * n4 + 255) / 256)), dim3(256), 0, st, x, y,
                            q, r, 4 * n4, n);
     return finish(check_launch("idiv"));
 }
@@ -291,8 +291,8 @@ static int32_t row_reduce_entry(bool is_max, const float *x, float *out, int64_t
     if (rows == 0) return PITON_OK;
     const int vec = aligned16(x) && (stride % 4 == 0 || rows == 1);
     const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-    if (is_max) hipLaunchKernelGGL(row_reduce_kernel<true>, grid, block, 0, (hipStream_t)stream, x, out, rows, n_cols, stride, vec);
-    else hipLaunchKernelGGL(row_reduce_kernel<false>, grid, block, 0, (hipStream_t)stream, x, out, rows, n_cols, stride, vec);
+    if (is_max) PITON_LAUNCH(row_reduce_kernel<true>, grid, block, 0, (hipStream_t)stream, x, out, rows, n_cols, stride, vec);
+    else PITON_LAUNCH(row_reduce_kernel<false>, grid, block, 0, (hipStream_t)stream, x, out, rows, n_cols, stride, vec);
     return finish(check_launch(what));
 }
 
@@ -321,10 +321,10 @@ int32_t piton_mi355x_transpose(const float *x, float *out, int64_t n_rows, int64
                      (stride_x % 4 == 0 || n_rows == 1) && (stride_out % 4 == 0 || n_cols == 1);
     if (vec) {
         const int64_t tr = (n_rows + kTrR - 1) / kTrR, tc = (n_cols + kTrC - 1) / kTrC;
-        hipLaunchKernelGGL(transpose_vec_kernel, dim3((unsigned)(tr * tc)), dim3(kTrT), 0, (hipStream_t)stream, x, out,
+        PITON_LAUNCH(transpose_vec_kernel, dim3((unsigned)(tr * tc)), dim3(kTrT), 0, (hipStream_t)stream, x, out,
                            n_rows, n_cols, stride_x, stride_out, tc);
     } else {
-        hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, (hipStream_t)stream,
+        PITON_LAUNCH(transpose_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, (hipStream_t)stream,
                            x, out, n_rows, n_cols, stride_x, stride_out, tiles_n);
     }
     return finish(check_launch("transpose"));

@@ -255,7 +255,7 @@ void launch_rows(int mode, int64_t wgs, hipStream_t st, float *out, const float 
         const int64_t cap = (int64_t)device_cu_count() * per_cu;
         grid = wgs < cap ? wgs : cap;
     }
-    hipLaunchKernelGGL((softmax_rows_kernel<CH, ALIGNED>), dim3((unsigned)grid), dim3(256), 0, st, out, in, in_rs,
+    PITON_LAUNCH((softmax_rows_kernel<CH, ALIGNED>), dim3((unsigned)grid), dim3(256), 0, st, out, in, in_rs,
                        out_rs, n, rows);
 }
 
@@ -296,10 +296,10 @@ extern "C" int32_t piton_mi355x_softmax(float *out, const float *in, int64_t in_
 #define PITON_SM_WG(CH, T)                                                                                          \
     do {                                                                                                            \
         if (aligned)                                                                                                \
-            hipLaunchKernelGGL((softmax_wg_kernel<CH, T, true>), dim3((unsigned)n_rows), dim3(T), 0, st, out, in,   \
+            PITON_LAUNCH((softmax_wg_kernel<CH, T, true>), dim3((unsigned)n_rows), dim3(T), 0, st, out, in,   \
                                in_row_stride, out_row_stride, (int)n);                                              \
         else                                                                                                        \
-            hipLaunchKernelGGL((softmax_wg_kernel<CH, T, false>), dim3((unsigned)n_rows), dim3(T), 0, st, out, in,  \
+            PITON_LAUNCH((softmax_wg_kernel<CH, T, false>), dim3((unsigned)n_rows), dim3(T), 0, st, out, in,  \
                                in_row_stride, out_row_stride, (int)n);                                              \
     } while (0)
     PITON_REQUIRE(mode != 2 || n_rows <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "softmax: too many rows");
@@ -314,7 +314,7 @@ extern "C" int32_t piton_mi355x_softmax(float *out, const float *in, int64_t in_
     else if (per_lane <= 32) PITON_SM_WG(8, 256);
     else if (per_lane <= 64) PITON_SM_WG(16, 256);
     else
-        hipLaunchKernelGGL(softmax_long_kernel, dim3((unsigned)n_rows), block, 0, st, out, in, in_row_stride,
+        PITON_LAUNCH(softmax_long_kernel, dim3((unsigned)n_rows), block, 0, st, out, in, in_row_stride,
                            out_row_stride, n);
 #undef PITON_SM_WG
 #undef PITON_SM

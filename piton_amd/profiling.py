@@ -50,18 +50,27 @@ def _one(pattern):
     return files[0]
 
 
-def kernel_stats(kt_dir):
-    """Per (kernel, grid) launch statistics from the per-dispatch trace."""
+def kernel_stats(kt_dir, timed_steps=0):
+    """Per (kernel, grid) launch statistics from the per-dispatch trace. With timed_steps, the
+    4096^3 matmul group also reports the average of its last `timed_steps` dispatches in
+    dispatch order: bench.py's timed region (its earlier dispatches are the untimed clock ramp
+    and warm-up)."""
     groups = {}
     for r in csv.DictReader(open(_one(os.path.join(kt_dir, "*_kernel_trace.csv")))):
         if "piton::" in r["Kernel_Name"]:
             key = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]))
-            groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+            groups.setdefault(key, []).append((int(r["Start_Timestamp"]),
+                                               int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
     rows = []
-    for (k, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        d = sorted(d)
-        rows.append(dict(kernel=k, grid=grid, calls=len(d), avg_ns=sum(d) / len(d), min_ns=d[0],
-                         median_ns=d[len(d) // 2], max_ns=d[-1], workload=BENCH.get((k, grid), ("",))[0]))
+    for (k, grid), td in sorted(groups.items(), key=lambda kv: -sum(d for _, d in kv[1])):
+        in_order = [d for _, d in sorted(td)]
+        d = sorted(in_order)
+        row = dict(kernel=k, grid=grid, calls=len(d), avg_ns=sum(d) / len(d), min_ns=d[0],
+                   median_ns=d[len(d) // 2], max_ns=d[-1], workload=BENCH.get((k, grid), ("",))[0])
+        if timed_steps and row["workload"] == "matmul 4096^3" and len(in_order) >= timed_steps:
+            last = in_order[-timed_steps:]
+            row["timed_avg_ns"] = sum(last) / len(last)
+        rows.append(row)
     return rows
 
 
@@ -75,7 +84,7 @@ def counters(pmc_dir, counter):
     return {k: sum(v) / len(v) for k, v in agg.items()}
 
 
-def summarize(kt_dir, fetch_dir, write_dir):
+def summarize(kt_dir, fetch_dir, write_dir, timed_steps=0):
     fetch, write = counters(fetch_dir, "FETCH_SIZE"), counters(write_dir, "WRITE_SIZE")
     cal = [k for k in fetch if k[0].startswith("add_vec4_kernel")]
     if not cal:
@@ -89,7 +98,7 @@ def summarize(kt_dir, fetch_dir, write_dir):
             traffic[label] = dict(kernel=k[0], grid=k[1], fetch_bytes=fetch[k] * f_fetch,
                                   write_bytes=write[k] * f_write,
                                   traffic_bytes=fetch[k] * f_fetch + write[k] * f_write, algorithmic_bytes=algo)
-    return kernel_stats(kt_dir), traffic, f_fetch, f_write
+    return kernel_stats(kt_dir, timed_steps), traffic, f_fetch, f_write
 
 
 def mfma_busy(pmc_dir, xcds=8, simds=1024):
@@ -117,6 +126,9 @@ def main(argv=None):
     ap.add_argument("fetch_dir", nargs="?")
     ap.add_argument("write_dir", nargs="?")
     ap.add_argument("--json")
+    ap.add_argument("--timed-steps", type=int, default=20,
+                    help="bench.py --steps of the traced run: the matmul's timed dispatches are its last ones")
+    ap.add_argument("--commit", default=None, help="the commit the traced runs were made at (recorded)")
     ap.add_argument("--mfma", action="store_true",
                     help="kt_dir is a --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES run: print MFMA occupancy")
     a = ap.parse_args(argv)
@@ -125,8 +137,16 @@ def main(argv=None):
         for label, m in mfma_busy(a.kt_dir).items():
             sys.stdout.write(f"| {label} | `{m['kernel']}` | {m['dispatches']} | {100 * m['mfma_busy']:.1f} % |\n")
         return
-    stats, traffic, ff, fw = summarize(a.kt_dir, a.fetch_dir, a.write_dir)
+    stats, traffic, ff, fw = summarize(a.kt_dir, a.fetch_dir, a.write_dir, a.timed_steps)
     out = sys.stdout
+    if a.commit:
+        out.write(f"Traced at commit {a.commit}.\n\n")
+    for r in stats:
+        if "timed_avg_ns" in r:
+            flops = BENCH[(r["kernel"], r["grid"])][2]
+            out.write(f"bench.py's timed region: the last {a.timed_steps} `{r['kernel']}` dispatches (after the "
+                      f"untimed clock ramp and warm-up) average {r['timed_avg_ns'] / 1e3:.2f} us = "
+                      f"{flops / r['timed_avg_ns'] / 1e3:.1f} TFLOP/s.\n\n")
     out.write("## Kernel durations (rocprofv3 --kernel-trace, per dispatch, grouped by grid)\n\n")
     out.write("| kernel | grid (work-items) | benchmark workload | calls | avg us | median us | min us | max us | "
               "achieved |\n|---|---|---|---|---|---|---|---|---|\n")
@@ -149,7 +169,7 @@ def main(argv=None):
                   f"{t['traffic_bytes'] / 1e6:.1f} | {algo / 1e6:.1f} | {t['traffic_bytes'] / algo:.2f} |\n")
     if a.json:
         with open(a.json, "w") as f:
-            json.dump(dict(fetch_factor=ff, write_factor=fw, kernels=traffic), f, indent=1)
+            json.dump(dict(commit=a.commit, fetch_factor=ff, write_factor=fw, kernels=traffic), f, indent=1)
 
 
 if __name__ == "__main__":

@@ -17,12 +17,13 @@ tiles in the reference) and is checked.
 from __future__ import annotations
 
 import inspect
+import os
 from dataclasses import dataclass, field
 
 import numpy as np
 
-from ..jit import cdiv
 from ..language import constexpr
+from .table import KERNELS, Arr, KernelSpec
 
 _DTYPE_SIG = {np.dtype(np.float32): "*fp32", np.dtype(np.int32): "*i32", np.dtype(np.uint32): "*u32"}
 
@@ -84,7 +85,15 @@ def bind(fn, args, kwargs, do_not_specialize=()):
 
 @dataclass
 class LaunchRecord:
-    """What a launch returns (the reference returns its CompiledKernel, launcher.py:245)."""
+    """What a launch returns (the reference returns its CompiledKernel with `last_stats` set from
+    the emulator's counters, launcher.py:238-245). `last_stats` holds:
+      * "launches": the device kernels the entry ran, each with its grid, block, LDS bytes,
+        vector registers and spill bytes (piton_mi355x_last_launches);
+      * "flops" / "bytes": the launch's algorithmic work (what the reference kernel computes,
+        read once and written once), the figures a roofline is computed from;
+      * "elapsed_us": the launch's time from HIP events around it, when PITON_MI355X_TIMING=1
+        (the call then waits for the launch);
+      * "num_stages": as passed."""
     name: str
     grid: tuple
     entry: str
@@ -93,168 +102,83 @@ class LaunchRecord:
     last_stats: dict = field(default_factory=dict)
 
 
-# -- kernel registry: name -> (parameter names, planner) -----------------------------------------
-# A planner checks the grid and the constexprs and returns (entry name in mi355x.py, args), where
-# Arr(name) stands for the array argument `name`; nothing touches the device before it returns.
+REGISTRY = KERNELS  # kernel name -> KernelSpec (piton_amd.runtime.table)
 
-class Arr:
-    __slots__ = ("name",)
 
-    def __init__(self, name):
-        self.name = name
+def lookup(jitfn) -> KernelSpec:
+    """The spec of a kernel, matched by name and parameter list."""
+    spec = KERNELS.get(jitfn.__name__)
+    if spec is None:
+        raise NotImplementedError(f"no mi355x kernel for {jitfn.__name__!r}; this backend provides "
+                                  f"{sorted(KERNELS)}")
+    if tuple(jitfn.arg_names) != spec.params:
+        raise NotImplementedError(f"{jitfn.__name__}{tuple(jitfn.arg_names)} does not match the mi355x "
+                                  f"kernel's parameters {spec.params}")
+    return spec
 
 
 def _grid3(grid):
     return tuple(int(g) for g in grid) + (1,) * (3 - len(grid))
 
 
-def _expect_grid(name, grid, want):
-    if _grid3(grid) != _grid3(want):
-        raise ValueError(f"{name}: grid {tuple(grid)} does not cover the kernel's tiles; expected {tuple(want)}")
-
-
-def _plan_matmul(a, grid):
-    M, N, K = int(a["M"]), int(a["N"]), int(a["K"])
-    _expect_grid("matmul_kernel", grid, (cdiv(M, a["BLOCK_SIZE_M"]) * cdiv(N, a["BLOCK_SIZE_N"]),))
-    return "matmul", (Arr("a_ptr"), Arr("b_ptr"), Arr("c_ptr"), M, N, K, int(a["stride_am"]), int(a["stride_ak"]),
-                      int(a["stride_bk"]), int(a["stride_bn"]), int(a["stride_cm"]), int(a["stride_cn"]),
-                      int(a["GROUP_SIZE_M"]))
-
-
-def _plan_softmax(a, grid):
-    g = _grid3(grid)
-    if g[1] != 1 or g[2] != 1:
-        raise ValueError(f"softmax_kernel: grid {tuple(grid)} must be (n_rows,)")
-    return "softmax", (Arr("output_ptr"), Arr("input_ptr"), int(a["input_row_stride"]), int(a["output_row_stride"]),
-                       int(a["n_cols"]), g[0], int(a["BLOCK_SIZE"]))
-
-
-def _plan_attn(a, grid):
-    n_ctx, heads = int(a["N_CTX"]), _grid3(grid)[1]
-    _expect_grid("attn_fwd_kernel", grid, (cdiv(n_ctx, a["BLOCK_M"]), heads))
-    if a["EVEN_N"] and n_ctx % int(a["BLOCK_N"]):
-        raise ValueError("attn_fwd_kernel: EVEN_N promises N_CTX % BLOCK_N == 0")
-    return "attn_fwd", (Arr("Q"), Arr("K"), Arr("V"), Arr("Out"), float(a["sm_scale"]), int(a["stride_qh"]),
-                        int(a["stride_qm"]), int(a["stride_kh"]), int(a["stride_kn"]), int(a["stride_kk"]),
-                        int(a["stride_vh"]), int(a["stride_vn"]), int(a["stride_oh"]), int(a["stride_om"]), n_ctx,
-                        heads, int(a["HEAD_DIM"]), bool(a["CAUSAL"]))
-
-
-def _plan_dense(a, grid):
-    M, N, K = int(a["M"]), int(a["N"]), int(a["K"])
-    _expect_grid("dense_layer_kernel", grid, (cdiv(M, a["BLOCK_SIZE_M"]) * cdiv(N, a["BLOCK_SIZE_N"]),))
-    add_bias = bool(a["ADD_BIAS"])
-    return "dense", (Arr("x_ptr"), Arr("w_ptr"), Arr("bias_ptr") if add_bias else None, Arr("y_ptr"), M, N, K,
-                     add_bias, bool(a["RELU"]))
-
-
-def _plan_add(a, grid):
-    n = int(a["n_elements"])
-    _expect_grid("add_kernel", grid, (cdiv(n, a["BLOCK_SIZE"]),))
-    return "add", (Arr("x_ptr"), Arr("y_ptr"), Arr("output_ptr"), n)
-
-
-def _plan_layernorm(a, grid):
-    g = _grid3(grid)
-    if g[1] != 1 or g[2] != 1:
-        raise ValueError(f"layernorm_kernel: grid {tuple(grid)} must be (rows,)")
-    block = int(a["BLOCK"])
-    return "layernorm", (Arr("x_ptr"), Arr("out_ptr"), min(int(a["n"]), block), float(a["eps"]), g[0], block)
-
-
-def _plan_map(entry, ptrs, scalars=()):
-    """An elementwise primitive: grid (cdiv(n, BLOCK),), arguments (pointers..., n, scalars...)."""
-    def plan(a, grid):
-        n = int(a["n"])
-        _expect_grid(entry + "_kernel", grid, (cdiv(n, a["BLOCK"]),))
-        return entry, (*[Arr(p) for p in ptrs], n, *[conv(a[s]) for s, conv in scalars])
-    return plan
-
-
-def _plan_row_reduce(entry):
-    def plan(a, grid):
-        g = _grid3(grid)
-        if g[1] != 1 or g[2] != 1:
-            raise ValueError(f"{entry}_kernel: grid {tuple(grid)} must be (rows / BLOCK_M,)")
-        # the reference reads whole BLOCK_N chunks of each row, unmasked (kernels.py:92-95)
-        cols = cdiv(int(a["n_cols"]), a["BLOCK_N"]) * int(a["BLOCK_N"])
-        return entry, (Arr("x_ptr"), Arr("out_ptr"), g[0] * int(a["BLOCK_M"]), cols, int(a["stride"]))
-    return plan
-
-
-def _plan_transpose(a, grid):
-    n_rows, n_cols = int(a["n_rows"]), int(a["n_cols"])
-    _expect_grid("transpose_kernel", grid, (cdiv(n_rows, a["BLOCK_M"]) * cdiv(n_cols, a["BLOCK_N"]),))
-    return "transpose", (Arr("x_ptr"), Arr("out_ptr"), n_rows, n_cols, int(a["stride_x"]), int(a["stride_out"]))
-
-
-REGISTRY = {
-    "matmul_kernel": (("a_ptr", "b_ptr", "c_ptr", "M", "N", "K", "stride_am", "stride_ak", "stride_bk",
-                       "stride_bn", "stride_cm", "stride_cn", "BLOCK_SIZE_M", "BLOCK_SIZE_N", "BLOCK_SIZE_K",
-                       "GROUP_SIZE_M"), _plan_matmul),
-    "softmax_kernel": (("output_ptr", "input_ptr", "input_row_stride", "output_row_stride", "n_cols",
-                        "BLOCK_SIZE"), _plan_softmax),
-    "attn_fwd_kernel": (("Q", "K", "V", "Out", "sm_scale", "stride_qh", "stride_qm", "stride_kh", "stride_kn",
-                         "stride_kk", "stride_vh", "stride_vn", "stride_oh", "stride_om", "N_CTX", "HEAD_DIM",
-                         "BLOCK_M", "BLOCK_N", "CAUSAL", "EVEN_N"), _plan_attn),
-    "dense_layer_kernel": (("x_ptr", "w_ptr", "bias_ptr", "y_ptr", "M", "N", "K", "BLOCK_SIZE_M", "BLOCK_SIZE_N",
-                            "BLOCK_SIZE_K", "GROUP_SIZE_M", "ADD_BIAS", "RELU"), _plan_dense),
-    "add_kernel": (("x_ptr", "y_ptr", "output_ptr", "n_elements", "BLOCK_SIZE"), _plan_add),
-    "layernorm_kernel": (("x_ptr", "out_ptr", "n", "eps", "BLOCK"), _plan_layernorm),
-    "copy_kernel": (("x_ptr", "out_ptr", "n", "BLOCK"), _plan_map("copy", ("x_ptr", "out_ptr"))),
-    "mul_kernel": (("x_ptr", "y_ptr", "out_ptr", "n", "BLOCK"), _plan_map("mul", ("x_ptr", "y_ptr", "out_ptr"))),
-    "fma_kernel": (("x_ptr", "y_ptr", "out_ptr", "n", "alpha", "BLOCK"),
-                   _plan_map("fma", ("x_ptr", "y_ptr", "out_ptr"), (("alpha", float),))),
-    "scaled_relu_kernel": (("x_ptr", "out_ptr", "n", "alpha", "BLOCK"),
-                           _plan_map("scaled_relu", ("x_ptr", "out_ptr"), (("alpha", float),))),
-    "sfu_kernel": (("x_ptr", "out_ptr", "n", "OP", "BLOCK"), _plan_map("sfu", ("x_ptr", "out_ptr"), (("OP", int),))),
-    "log_kernel": (("x_ptr", "out_ptr", "n", "BLOCK"), _plan_map("log", ("x_ptr", "out_ptr"))),
-    "idiv_kernel": (("x_ptr", "y_ptr", "q_ptr", "r_ptr", "n", "BLOCK"),
-                    _plan_map("idiv", ("x_ptr", "y_ptr", "q_ptr", "r_ptr"))),
-    "row_sum_kernel": (("x_ptr", "out_ptr", "n_cols", "stride", "BLOCK_M", "BLOCK_N"), _plan_row_reduce("row_sum")),
-    "row_max_kernel": (("x_ptr", "out_ptr", "n_cols", "stride", "BLOCK_M", "BLOCK_N"), _plan_row_reduce("row_max")),
-    "transpose_kernel": (("x_ptr", "out_ptr", "n_rows", "n_cols", "stride_x", "stride_out", "BLOCK_M", "BLOCK_N"),
-                         _plan_transpose),
-}
-
-
-def lookup(jitfn):
-    """The planner of a kernel, matched by name and parameter list."""
-    entry = REGISTRY.get(jitfn.__name__)
-    if entry is None:
-        raise NotImplementedError(f"no mi355x kernel for {jitfn.__name__!r}; this backend provides "
-                                  f"{sorted(REGISTRY)}")
-    params, planner = entry
-    if tuple(jitfn.arg_names) != params:
-        raise NotImplementedError(f"{jitfn.__name__}{tuple(jitfn.arg_names)} does not match the mi355x "
-                                  f"kernel's parameters {params}")
-    return planner
+def _env(grid, constants, values):
+    env = dict(values, **constants)
+    env["grid"] = _grid3(grid)
+    return env
 
 
 def plan(jitfn, grid, constants, values):
-    """(entry, args) of a launch, with every host-side check done."""
-    return lookup(jitfn)(dict(values, **constants), grid)
+    """(entry, args) of a launch, with every host-side check done: the grid must be the kernel's
+    canonical cover (any other grid would compute a different set of tiles in the reference)."""
+    spec = lookup(jitfn)
+    env = _env(grid, constants, values)
+    want = spec.expected_grid(env)
+    if any(w is not None and w != g for w, g in zip(want, env["grid"])):
+        shown = tuple("any" if w is None else w for w in want)
+        raise ValueError(f"{jitfn.__name__}: grid {tuple(grid)} does not cover the kernel's tiles; expected {shown}")
+    for cond, msg in spec.checks:
+        if not cond.py(env):
+            raise ValueError(f"{jitfn.__name__}: {msg}")
+    return spec.entry, spec.args(env)
+
+
+def _timing() -> bool:
+    return os.environ.get("PITON_MI355X_TIMING", "") not in ("", "0")
 
 
 def run_mi355x(jitfn, grid, signature, constants, values) -> LaunchRecord:
-    """Launch on the MI355X library: stage numpy arrays, call the entry, copy arrays back."""
+    """Launch on the MI355X library: stage numpy arrays, call the entry, copy arrays back.
+
+    `jitfn` needs only what the reference's JITFunction carries (piton/jit.py:16-25): `__name__`
+    and `arg_names`; `signature`, `constants` and `values` are what the reference's `bind`
+    returns for the launch (launcher.py:42-63) and `grid` the resolved grid tuple."""
     entry, args = plan(jitfn, grid, constants, values)
     import torch
 
     from . import mi355x as rt
+    dev = rt.staging_device()
     staged = {}
     for name, v in values.items():
         if isinstance(v, np.ndarray):
             flat = np.ascontiguousarray(v).reshape(-1)
-            staged[name] = torch.from_numpy(flat.view(np.int32) if v.dtype == np.uint32 else flat).to("cuda")
+            staged[name] = torch.from_numpy(flat.view(np.int32) if v.dtype == np.uint32 else flat).to(dev)
     resolved = [(staged.get(x.name, values.get(x.name)) if isinstance(x, Arr) else x) for x in args]
+    timed = _timing()
+    if timed:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
     getattr(rt, entry)(*resolved)
+    stats = {"launches": rt.last_launches(), **lookup(jitfn).work(_env(grid, constants, values))}
+    if timed:
+        e1.record()
+        e1.synchronize()
+        stats["elapsed_us"] = e0.elapsed_time(e1) * 1e3
     if staged:
-        torch.cuda.current_stream().synchronize()
-        for name, dev in staged.items():
+        rt.synchronize()
+        for name, t in staged.items():
             v = values[name]
-            v[...] = dev.cpu().numpy().view(v.dtype).reshape(v.shape)
-    return LaunchRecord(jitfn.__name__, tuple(grid), "piton_mi355x_" + entry, signature, constants)
+            v[...] = t.cpu().numpy().view(v.dtype).reshape(v.shape)
+    return LaunchRecord(jitfn.__name__, tuple(grid), "piton_mi355x_" + entry, signature, constants, stats)
 
 
 class Launcher:
@@ -273,6 +197,6 @@ class Launcher:
         grid = tuple(grid) if isinstance(grid, (tuple, list)) else (grid,)
         if device == "mi355x":
             rec = run_mi355x(self.jitfn, grid, signature, constants, values)
-            rec.last_stats = {"num_stages": num_stages}
+            rec.last_stats["num_stages"] = num_stages
             return rec
         raise ValueError(f"unknown device {device!r}")

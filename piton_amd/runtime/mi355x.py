@@ -40,9 +40,15 @@ class DeviceInfo(ctypes.Structure):
                 ("xcd_count", ctypes.c_int32), ("arch", ctypes.c_char * 64)]
 
 
+class LaunchInfo(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_char * 96), ("grid", ctypes.c_uint32 * 3), ("block", ctypes.c_uint32 * 3),
+                ("lds_bytes", ctypes.c_uint32), ("vgprs", ctypes.c_int32), ("scratch_bytes", ctypes.c_uint32)]
+
+
 # entry name -> argtypes (every entry returns int32)
 SIGNATURES = {
     "piton_mi355x_device_info": [ctypes.POINTER(DeviceInfo)],
+    "piton_mi355x_last_launches": [ctypes.POINTER(LaunchInfo), _i32, ctypes.POINTER(_i32)],
     "piton_mi355x_matmul": [_p, _p, _p] + [_i64] * 9 + [_i32, _p],
     "piton_mi355x_softmax": [_p, _p] + [_i64] * 5 + [_p],
     "piton_mi355x_attn_fwd": [_p, _p, _p, _p, _f32] + [_i64] * 11 + [_i32, _i32, _p],
@@ -124,6 +130,26 @@ def device_info() -> dict:
     d = {k: getattr(info, k) for k, _ in DeviceInfo._fields_}
     d["arch"] = info.arch.decode()
     return d
+
+
+def last_launches() -> list:
+    """The kernel launches of this thread's last entry call: kernel name, grid, block, LDS bytes
+    per workgroup, vector registers and spill bytes per lane."""
+    infos = (LaunchInfo * 8)()
+    n = ctypes.c_int32(0)
+    _call("piton_mi355x_last_launches", infos, 8, ctypes.byref(n))
+    return [{"kernel": i.kernel.decode(), "grid": tuple(i.grid), "block": tuple(i.block), "lds_bytes": i.lds_bytes,
+             "vgprs": i.vgprs, "scratch_bytes": i.scratch_bytes} for i in infos[:min(n.value, 8)]]
+
+
+def staging_device() -> str:
+    """Where numpy arguments of a launch are copied before the call."""
+    return "cuda"
+
+
+def synchronize() -> None:
+    """Waits for the work queued on torch's current stream."""
+    torch.cuda.current_stream().synchronize()
 
 
 # -- argument checks ---------------------------------------------------------------------------

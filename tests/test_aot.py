@@ -1,7 +1,7 @@
 """The AOT C launchers (piton_amd/aot.py; piton/tools/compile.py:55-172 is the reference's):
 generated headers and sources compile as C, the grid check refuses other covers before any
-device call, the launch reaches the library, and on a GPU a C launcher computes what the
-Python launch surface computes."""
+device call, the launch reaches the library, and on a GPU the C launchers' results match float64
+and the oracle at config shapes."""
 import ctypes
 import os
 import shutil
@@ -23,7 +23,7 @@ MATMUL_CONST = "stride_ak=1,stride_bn=1,stride_cn=1,BLOCK_SIZE_M=128,BLOCK_SIZE_
 SPECS = {
     "matmul_kernel": (MATMUL_SIG, MATMUL_CONST),
     "softmax_kernel": ("output_ptr=*fp32,input_ptr=*fp32,input_row_stride=i32,output_row_stride=i32,n_cols=i32",
-                       "BLOCK_SIZE=1024"),
+                       "BLOCK_SIZE=2048"),
     "attn_fwd_kernel": ("Q=*fp32,K=*fp32,V=*fp32,Out=*fp32,sm_scale=fp32,stride_qh=i32,stride_qm=i32,stride_kh=i32,"
                         "stride_kn=i32,stride_vh=i32,stride_vn=i32,stride_oh=i32,stride_om=i32,N_CTX=i32",
                         "stride_kk=1,HEAD_DIM=64,BLOCK_M=32,BLOCK_N=32,CAUSAL=True,EVEN_N=False"),
@@ -106,7 +106,7 @@ int main(void) {
 
 
 def test_bad_specifications_are_refused():
-    params = aot.KERNELS["add_kernel"]["params"]
+    params = aot.KERNELS["add_kernel"].params
     with pytest.raises(TypeError, match="missing"):
         aot.emit_c("add_kernel", params, {"x_ptr": "*fp32"}, {}, "x")
     with pytest.raises(TypeError, match="unsupported type"):
@@ -119,47 +119,94 @@ def test_bad_specifications_are_refused():
         aot.emit_c("nope_kernel", params, {}, {}, "x")
 
 
-@pytest.mark.gpu
-def test_c_launchers_compute_what_the_launch_surface_computes(tmp_path):
-    """matmul and softmax through generated C launchers (built into a shared object, called
-    with device pointers) equal the ctypes launch of the same library bit for bit."""
-    import torch
-    srcs = [generate(tmp_path, "matmul_kernel", "matmul"), generate(tmp_path, "softmax_kernel", "softmax")]
+def _launchers(tmp_path, kernels):
+    srcs = [generate(tmp_path, k, k.replace("_kernel", "")) for k in kernels]
     so = tmp_path / "liblaunchers.so"
     r = subprocess.run([GCC, *cflags(), "-fPIC", "-shared", *srcs, "-o", str(so), *link_flags()],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
-    L = ctypes.CDLL(str(so))
-    M, N, K = 300, 200, 72
-    g = torch.Generator(device="cuda").manual_seed(3)
-    a, b = torch.rand((M, K), device="cuda", generator=g), torch.rand((K, N), device="cuda", generator=g)
-    c_aot, c_ref = torch.zeros((M, N), device="cuda"), torch.zeros((M, N), device="cuda")
+    return ctypes.CDLL(str(so))
 
-    class MatmulArgs(ctypes.Structure):
-        _fields_ = [("a_ptr", ctypes.c_void_p), ("b_ptr", ctypes.c_void_p), ("c_ptr", ctypes.c_void_p),
-                    ("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32),
-                    ("stride_am", ctypes.c_int32), ("stride_bk", ctypes.c_int32), ("stride_cm", ctypes.c_int32)]
 
-    args = MatmulArgs(a.data_ptr(), b.data_ptr(), c_aot.data_ptr(), M, N, K, K, N, N)
-    usec = ctypes.c_uint32(0)
-    torch.cuda.synchronize()
-    assert L.matmul_launch_us(ctypes.byref(args), 3 * 2, 1, 1, ctypes.byref(usec)) == 0
-    mi355x.matmul(a, b, c_ref, M, N, K, K, 1, N, 1, N, 1, 8)
-    torch.cuda.synchronize()
-    assert torch.equal(c_aot, c_ref)
-    assert usec.value >= 0
+def _struct(kernel):
+    """The ctypes twin of a generated <name>_args_t (fields in --signature order)."""
+    sig, _ = SPECS[kernel]
+    ctype = {"*fp32": ctypes.c_void_p, "*i32": ctypes.c_void_p, "i32": ctypes.c_int32, "fp32": ctypes.c_float}
+    fields = [(n, ctype[t]) for n, t in (item.split("=") for item in sig.split(","))]
+    return type(kernel + "_args", (ctypes.Structure,), {"_fields_": fields})
 
-    class SoftmaxArgs(ctypes.Structure):
-        _fields_ = [("output_ptr", ctypes.c_void_p), ("input_ptr", ctypes.c_void_p),
-                    ("input_row_stride", ctypes.c_int32), ("output_row_stride", ctypes.c_int32),
-                    ("n_cols", ctypes.c_int32)]
 
-    x = torch.randn((64, 1000), device="cuda", generator=g)
-    y_aot, y_ref = torch.zeros_like(x), torch.zeros_like(x)
-    sargs = SoftmaxArgs(y_aot.data_ptr(), x.data_ptr(), 1000, 1000, 1000)
+@pytest.mark.gpu
+def test_c_launchers_against_the_oracle(tmp_path):
+    """Config shapes through generated C launchers, called with device pointers: the ragged
+    1000 x 1800 x 700 matmul with padded row strides, softmax over 1823 columns (BLOCK_SIZE
+    2048), causal attention, and the dense layer; each checked against float64 and the oracle
+    (the emulator's arithmetic), and bit-identical to the ctypes launch of the same library."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from oracle import fp64
+    L = _launchers(tmp_path, ["matmul_kernel", "softmax_kernel", "attn_fwd_kernel", "dense_layer_kernel"])
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    assert L.softmax_launch(ctypes.byref(sargs), 64, 1, 1, stream) == 0
-    mi355x.softmax(y_ref, x, 1000, 1000, 1000, 64, 1024)
+    rng = np.random.default_rng(11)
+
+    # matmul, ragged with padded strides (lda 703, ldb 1805, ldc 1807)
+    M, N, K, lda, ldb, ldc = 1000, 1800, 700, 703, 1805, 1807
+    a = rng.uniform(-1, 1, (M, lda)).astype(np.float32)
+    b = rng.uniform(-1, 1, (K, ldb)).astype(np.float32)
+    ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    tc, tc2 = (torch.full((M, ldc), -3.0, device="cuda") for _ in range(2))
+    args = _struct("matmul_kernel")(ta.data_ptr(), tb.data_ptr(), tc.data_ptr(), M, N, K, lda, ldb, ldc)
+    assert L.matmul_launch(ctypes.byref(args), 8 * 15, 1, 1, stream) == 0
+    assert L.matmul_launch(ctypes.byref(args), 8 * 15 + 1, 1, 1, stream) == -1
+    mi355x.matmul(ta, tb, tc2, M, N, K, lda, 1, ldb, 1, ldc, 1, 8)
     torch.cuda.synchronize()
-    assert torch.equal(y_aot, y_ref)
-    assert L.softmax_launch(ctypes.byref(sargs), 64, 2, 1, stream) == -1
+    assert torch.equal(tc, tc2)
+    c = tc.cpu().numpy()
+    assert (c[:, N:] == -3.0).all()
+    ref = fp64.matmul(a[:, :K], b[:, :N])
+    assert fp64.rel_fro(c[:, :N], ref) <= 1e-5
+    rows = slice(0, 64)
+    orc = np.asarray(oracle.matmul_fast(np.ascontiguousarray(a[rows, :K]), np.ascontiguousarray(b[:, :N])))
+    assert fp64.rel_fro(c[rows, :N], ref[rows]) <= fp64.rel_fro(orc, ref[rows])
+
+    # softmax, 1823 columns
+    x = (rng.standard_normal((257, 1823)) * 4).astype(np.float32)
+    tx = torch.from_numpy(x).cuda()
+    ty, ty2 = torch.zeros_like(tx), torch.zeros_like(tx)
+    sargs = _struct("softmax_kernel")(ty.data_ptr(), tx.data_ptr(), 1823, 1823, 1823)
+    assert L.softmax_launch(ctypes.byref(sargs), 257, 1, 1, stream) == 0
+    mi355x.softmax(ty2, tx, 1823, 1823, 1823, 257, 2048)
+    torch.cuda.synchronize()
+    assert torch.equal(ty, ty2)
+    err = fp64.rel_fro(ty.cpu().numpy(), fp64.softmax(x))
+    assert err <= 1e-5 and err <= fp64.rel_fro(oracle.softmax(x, 1823, 2048), fp64.softmax(x))
+
+    # causal attention, 4 heads x 256 x 64
+    H, Nc, D = 4, 256, 64
+    q, k, v = (rng.standard_normal((H, Nc, D)).astype(np.float32) for _ in range(3))
+    tq, tk, tv = (torch.from_numpy(t).cuda() for t in (q, k, v))
+    to = torch.zeros_like(tq)
+    at = _struct("attn_fwd_kernel")(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), to.data_ptr(), 0.125, Nc * D, D,
+                                    Nc * D, D, Nc * D, D, Nc * D, D, Nc)
+    assert L.attn_fwd_launch(ctypes.byref(at), Nc // 32, H, 1, stream) == 0
+    torch.cuda.synchronize()
+    ref = fp64.attention_reference(q, k, v, True, 0.125)
+    err = fp64.rel_fro(to.cpu().numpy(), ref)
+    assert err <= 1e-5 and err <= fp64.rel_fro(oracle.attention(q, k, v, True, 0.125, block_n=32), ref)
+
+    # dense + bias + ReLU (N = 128, K = 64 specialised), dyadic inputs: bit-exact
+    m = 1797
+    xd = (rng.integers(-4, 5, (m, 64)) / 4).astype(np.float32)
+    wd = (rng.integers(-4, 5, (64, 128)) / 4).astype(np.float32)
+    bd = (rng.integers(-8, 9, 128) / 4).astype(np.float32)
+    txd, twd, tbd = (torch.from_numpy(t).cuda() for t in (xd, wd, bd))
+    yd = torch.zeros((m, 128), device="cuda")
+    dargs = _struct("dense_layer_kernel")(txd.data_ptr(), twd.data_ptr(), tbd.data_ptr(), yd.data_ptr(), m)
+    assert L.dense_launch(ctypes.byref(dargs), (m + 3) // 4 * 2, 1, 1, stream) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(yd.cpu().numpy(), oracle.dense(xd, wd, bd, True))
+
+    usec = ctypes.c_uint32(0)
+    assert L.matmul_launch_us(ctypes.byref(args), 8 * 15, 1, 1, ctypes.byref(usec)) == 0 and usec.value > 0

@@ -37,3 +37,36 @@ def test_cpu_baseline_on_a_small_sample():
     # float32-rounded float64 products: a few ulp; the oracle's round-toward-zero chain: more
     err = res["err_vs_fp64"]
     assert err["rows"] == 16 and err["gpu"] < 1e-7 and 0 < err["oracle"] < 1e-5
+
+
+def test_cpu_legs_of_the_other_workloads_on_small_samples():
+    """Each workload's CPU leg (the oracle at one and several threads, numpy float64, errors of
+    the GPU's output and of the oracle's against float64) on a small synthetic sample, with the
+    float64 result standing in for the GPU's."""
+    import bench
+    from oracle import fp64
+    from piton_amd import digits
+    rng = np.random.default_rng(1)
+    n = 100
+    x = (rng.standard_normal((19, n)) * 4).astype(np.float32)
+    x[1, 5], x[2, 7], x[3] = np.inf, -np.inf, -np.inf
+    sm = bench.cpu_softmax(n, (x, fp64.softmax(x).astype(np.float32)), budget_s=0.05)
+    assert sm["oracle"]["value"] > 0 and sm["oracle_1_thread"]["threads"] == 1 and sm["numpy_fp64"]["value"] > 0
+    assert sm["err_vs_fp64"]["rows"] == 16 and sm["err_vs_fp64"]["gpu"] < 1e-7 < sm["err_vs_fp64"]["oracle"] < 1e-5
+    assert sm["special_rows_match_oracle"]
+
+    q, k, v = (rng.standard_normal((2, 64, 16)).astype(np.float32) for _ in range(3))
+    o = np.stack([fp64.attention_reference(q[h], k[h], v[h], True, 0.25) for h in range(2)]).astype(np.float32)
+    at = bench.cpu_attention((q, k, v, o), budget_s=0.05)
+    assert at["oracle"]["value"] > 0 and at["oracle"]["threads"] <= 2 and at["oracle_1_thread"]["value"] > 0
+    assert at["err_vs_fp64"]["gpu"] < 1e-7 < at["err_vs_fp64"]["oracle"] < 1e-5
+
+    layers = digits.he_normal_mlp(seed=1729)
+    xd = rng.integers(0, 17, (200, 64)).astype(np.float32)
+    h = xd.astype(np.float64)
+    for i, (w, b) in enumerate(layers):
+        h = fp64.dense(h, w, b, i < 2)
+    ml = bench.cpu_mlp((layers, xd, h.astype(np.float32), np.argmax(h, 1).astype(np.int32)), budget_s=0.05)
+    assert ml["oracle"]["value"] > 0 and ml["predictions_equal_oracle"] >= 198
+    assert ml["err_vs_fp64"]["oracle"] < 1e-5
+    assert bench.host_info()["cpu_count"] >= 1

@@ -15,6 +15,7 @@ import piton_amd
 from piton_amd import language as tl
 from piton_amd.kernels import attn_fwd_kernel, matmul_kernel, softmax_kernel
 from piton_amd.runtime import launcher, mi355x
+from ref_launch import RefJIT, patched_reference_call, ref_add_kernel, ref_matmul_kernel
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -172,3 +173,74 @@ def test_tensor_checks():
     with pytest.raises(TypeError):
         mi355x.check_tensor("x", t.double())
     assert mi355x._span((4, 10), (3, 1)) == 32 and mi355x._span((0, 5)) == -1
+
+
+# -- the reference-side hunks driven on any host ------------------------------------
+
+@pytest.fixture
+def host_entries(monkeypatch):
+    """The library's entries replaced by host computations on CPU tensors, so that the binding,
+    grid check, staging and copy-back run on a machine without a GPU."""
+    calls = []
+
+    def add(x, y, out, n):
+        calls.append(("add", x, y, out, n))
+        out[:n] = x[:n] + y[:n]
+
+    def matmul(a, b, c, M, N, K, s_am, s_ak, s_bk, s_bn, s_cm, s_cn, group):
+        calls.append(("matmul", M, N, K, s_am, s_ak, s_bk, s_bn, s_cm, s_cn, group))
+        A = torch.as_strided(a, (M, K), (s_am, s_ak))
+        B = torch.as_strided(b, (K, N), (s_bk, s_bn))
+        torch.as_strided(c, (M, N), (s_cm, s_cn)).copy_(A @ B)
+
+    monkeypatch.setattr(mi355x, "staging_device", lambda: "cpu")
+    monkeypatch.setattr(mi355x, "synchronize", lambda: None)
+    monkeypatch.setattr(mi355x, "last_launches", lambda: [{"kernel": "host"}])
+    monkeypatch.setattr(mi355x, "add", add)
+    monkeypatch.setattr(mi355x, "matmul", matmul)
+    return calls
+
+
+def test_reference_jit_object_with_numpy_arguments(host_entries):
+    """numpy arrays are copied in and every array is copied back (launcher.py:175-180, 209-211);
+    the grid is a callable of the launch's meta-parameters."""
+    k = RefJIT(ref_add_kernel)
+    n = 37
+    x = np.arange(n, dtype=np.float32)
+    y = np.full(n, 0.5, np.float32)
+    out = np.full(n + 16, 7.0, np.float32)
+    rec = patched_reference_call(k, lambda meta: (piton_amd.cdiv(n, meta["BLOCK_SIZE"]),), x, y, out, n,
+                                 BLOCK_SIZE=16)
+    np.testing.assert_array_equal(out[:n], x + y)
+    assert (out[n:] == 7.0).all()
+    np.testing.assert_array_equal(x, np.arange(n, dtype=np.float32))
+    name, tx, ty, tout, nn = host_entries[0]
+    assert name == "add" and nn == n and tx.device.type == "cpu" and tout.numel() == n + 16
+    assert rec.entry == "piton_mi355x_add" and rec.grid == (3,) and rec.signature["x_ptr"] == "*fp32"
+    assert rec.last_stats["bytes"] == 12 * n and rec.last_stats["launches"] == [{"kernel": "host"}]
+
+
+def test_reference_jit_object_with_tensors_and_unit_strides(host_entries):
+    """Tensor arguments pass through by reference; strides equal to 1 arrive as constants and
+    still reach the entry; the grid is checked before the entry is called."""
+    k = RefJIT(ref_matmul_kernel)
+    M, N, K = 5, 7, 3
+    a = torch.arange(M * K, dtype=torch.float32).reshape(M, K)
+    b = torch.ones(K, N)
+    c = torch.zeros(M, N)
+    kw = dict(BLOCK_SIZE_M=4, BLOCK_SIZE_N=4, BLOCK_SIZE_K=4, GROUP_SIZE_M=8, num_warps=4)
+    args = (a, b, c, M, N, K, K, 1, N, 1, N, 1)
+    with pytest.raises(ValueError, match="grid"):
+        patched_reference_call(k, (3,), *args, **kw)
+    assert host_entries == []
+    rec = patched_reference_call(k, (4,), *args, **kw)
+    assert host_entries[0] == ("matmul", M, N, K, K, 1, N, 1, N, 1, 8)
+    torch.testing.assert_close(c, a @ b)
+    assert rec.constants["stride_ak"] == 1 and rec.last_stats["flops"] == 2 * M * N * K
+
+
+def test_reference_sig_of_rejects_other_tensor_dtypes():
+    k = RefJIT(ref_add_kernel)
+    x = torch.zeros(4, dtype=torch.float64)
+    with pytest.raises(TypeError, match="tensor dtype"):
+        patched_reference_call(k, (1,), x, x, x, 4, BLOCK_SIZE=4)

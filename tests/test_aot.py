@@ -204,7 +204,7 @@ def test_c_launchers_against_the_oracle(tmp_path):
     txd, twd, tbd = (torch.from_numpy(t).cuda() for t in (xd, wd, bd))
     yd = torch.zeros((m, 128), device="cuda")
     dargs = _struct("dense_layer_kernel")(txd.data_ptr(), twd.data_ptr(), tbd.data_ptr(), yd.data_ptr(), m)
-    assert L.dense_launch(ctypes.byref(dargs), (m + 3) // 4 * 2, 1, 1, stream) == 0
+    assert L.dense_layer_launch(ctypes.byref(dargs), (m + 3) // 4 * 2, 1, 1, stream) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(yd.cpu().numpy(), oracle.dense(xd, wd, bd, True))
 

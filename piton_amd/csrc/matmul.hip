@@ -439,6 +439,154 @@ void gemm_direct_kernel(GemmArgs g) {
         }
 }
 
+// Row-major shapes with too few 128 x 128 tiles to fill the chip (config 2's 512^3 has 16 and
+// 1024^3 64 for 256 CUs) or with ragged edges: a workgroup owns a TB x TB tile (TB = 32 NB) and
+// its KS waves split K, each wave computing the whole tile, NB x NB blocks of
+// v_mfma_f32_32x32x2_f32, over the K tiles kt = wave, wave + KS, ... (interleaved, so the waves
+// read neighbouring k together). Operands go from memory straight into registers as in the
+// direct kernel (the same k order inside a K tile of 32: lane half h supplies k = 16 h + s at
+// step s), through buffer descriptors bounded at each matrix's last element: rows of A past M
+// and rows of B past K read as zeros, and the K tail of A (k >= K inside the last tile, which
+// may hold padding or the next row) is zeroed before its products, as the reference's K mask
+// does. The KS partial tiles meet in LDS and add in wave order (fixed: the result does not
+// depend on timing); the epilogue (bias, ReLU, residual) then stores rows < M and columns < N.
+// AVEC: A rows 16-byte aligned (16-byte loads of A); otherwise 4-byte loads.
+constexpr int kMaxSplitWaves = 4;
+
+template <int NB, int KS, bool AVEC>
+__global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
+    constexpr int TB = 32 * NB;
+    constexpr int NACC = NB * NB * 16;  // accumulator registers per lane
+    __shared__ float red[KS > 1 ? KS : 1][NACC][64];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int half = lane >> 5, l31 = lane & 31;
+
+    const int num_pid_m = (int)((g.M + TB - 1) / TB);
+    const int num_pid_n = (int)((g.N + TB - 1) / TB);
+    const int pid = xcd_logical_id(blockIdx.x, gridDim.x, kXcdCount);
+    const int in_group = g.group_m * num_pid_n;
+    const int group_id = pid / in_group;
+    const int first_m = group_id * g.group_m;
+    const int gsize = min(num_pid_m - first_m, g.group_m);
+    const int pid_m = first_m + (pid % in_group) % gsize;
+    const int pid_n = (pid % in_group) / gsize;
+    const int64_t m0 = (int64_t)pid_m * TB, n0 = (int64_t)pid_n * TB;
+
+    // bounded at the last element of each matrix: offsets at or past the bound read as zero
+    const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.a), (short)0,
+                                                      (int)(((g.M - 1) * g.s_am + g.K) * 4), 0x00020000);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.b), (short)0,
+                                                      (int)(((g.K - 1) * g.s_bk + g.N) * 4), 0x00020000);
+    uint32_t va[NB], vb[NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++) va[i] = (uint32_t)(((m0 + i * 32 + l31) * g.s_am + 16 * half) * 4);
+#pragma unroll
+    for (int j = 0; j < NB; j++) vb[j] = (uint32_t)(((int64_t)(16 * half) * g.s_bk + n0 + j * 32 + l31) * 4);
+    const uint32_t sbk4 = (uint32_t)(g.s_bk * 4);
+    const int nk = (int)((g.K + 31) / 32);
+    const int k_tail = (int)(g.K - (int64_t)(nk - 1) * 32);  // valid k of the last tile, 1..32
+
+    struct Ops {
+        float a[NB][16];
+        float b[NB][16];
+    };
+    // every offset goes in the per-lane address, which is what the descriptor's range check covers
+    auto load = [&](int kt, Ops &o) {
+        const uint32_t ka = (uint32_t)kt * 128u, kb = (uint32_t)kt * 32u * sbk4;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            if constexpr (AVEC) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 v = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(va[i] + ka + 16 * q), 0, 0));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o.a[i][4 * q + e] = v[e];
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 16; s++)
+                    o.a[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)(va[i] + ka + 4 * s), 0, 0));
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; s++)
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+                o.b[j][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)(vb[j] + kb + s * sbk4), 0, 0));
+    };
+    f32x16 acc[NB][NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+    auto mul = [&](Ops &o, int kt) {
+        if (kt == nk - 1 && k_tail < 32) {
+            // the K tail: this lane's k = 16 half + s past K contributes nothing
+#pragma unroll
+            for (int s = 0; s < 16; s++)
+                if (16 * half + s >= k_tail)
+#pragma unroll
+                    for (int i = 0; i < NB; i++) o.a[i][s] = 0.f;
+        }
+#pragma unroll
+        for (int s = 0; s < 16; s++)
+#pragma unroll
+            for (int i = 0; i < NB; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i][s], o.b[j][s], acc[i][j], 0, 0, 0);
+    };
+    // this wave's K tiles: wave, wave + KS, ...; the next one is in flight while one multiplies.
+    // The prefetch past the last tile reads at or beyond the descriptors' bounds (zeros) or
+    // inside the matrices, and is never used.
+    Ops o0, o1;
+    load(wave, o0);
+    for (int kt = wave; kt < nk; kt += 2 * KS) {
+        load(kt + KS, o1);
+        mul(o0, kt);
+        if (kt + KS >= nk) break;
+        load(kt + 2 * KS, o0);
+        mul(o1, kt + KS);
+    }
+
+    // accumulator r of a 32x32 block holds row 8*(r/4) + 4*half + r%4, column l31
+    auto store = [&](int i, int j, int r, int ln, float v) {
+        const int64_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
+        const int64_t col = n0 + j * 32 + (ln & 31);
+        if (row >= g.M || col >= g.N) return;
+        if (g.bias) v += g.bias[col];
+        if (g.relu && v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
+        if (g.res) v += g.res[row * g.s_rm + col];
+        g.c[row * g.s_cm + col * g.s_cn] = v;
+    };
+    if constexpr (KS == 1) {
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) store(i, j, r, lane, acc[i][j][r]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) red[wave][(i * NB + j) * 16 + r][lane] = acc[i][j][r];
+        __syncthreads();
+        // wave w finishes accumulator slots w, w + KS, ...: the partials add in wave order
+        for (int x = wave; x < NACC; x += KS) {
+            float v = red[0][x][lane];
+#pragma unroll
+            for (int w = 1; w < KS; w++) v += red[w][x][lane];
+            store((x >> 4) / NB, (x >> 4) % NB, x & 15, lane, v);
+        }
+    }
+}
+
 // First index of the largest of x[r, 0:n] (numpy argmax rule: the first NaN wins), one wave
 // per row: each lane scans elements lane, lane + 64, ..., then the (value, index) pairs combine
 // across the wave. The combine (a NaN beats any number, the larger value beats the smaller,
@@ -607,6 +755,45 @@ static int layout_b(const GemmArgs &g) {
     return SCALAR;
 }
 
+// The split kernel's tile (NB blocks of 32 per side) and waves per workgroup for a row-major
+// shape, or nb = 0 when it does not apply. Tiles of 64 when there are at least as many as
+// CUs, else of 32; then the waves double (up to kMaxSplitWaves) until the launch has four
+// waves per CU, as long as each wave keeps at least two K tiles.
+struct SplitPlan {
+    int nb, ks;
+    int64_t tiles;
+};
+static SplitPlan plan_split(const GemmArgs &g, int cus) {
+    SplitPlan p{0, 0, 0};
+    if (g.s_ak != 1 || g.s_bn != 1 || g.s_am <= 0 || g.s_bk <= 0 || g.K <= 0 || g.M <= 0 || g.N <= 0) return p;
+    auto tiles = [&](int64_t tb) { return ((g.M + tb - 1) / tb) * ((g.N + tb - 1) / tb); };
+    const int64_t nk = (g.K + 31) / 32;
+    const int nb = tiles(64) >= cus ? 2 : 1;
+    const int64_t nt = tiles(32 * nb);
+    int ks = 1;
+    while (ks < kMaxSplitWaves && nt * ks < 4 * (int64_t)cus && 4 * ks <= nk) ks *= 2;
+    // every byte offset a lane forms (the prefetch past the last tile included) stays below 2^31
+    const int64_t tb = 32 * nb, kpad = g.K + 32 * (2 * ks + 3);  // the farthest prefetch: tile nk - 1 + 2 ks
+    if (((g.M + tb) * g.s_am + kpad) * 4 >= (1LL << 31) || (kpad * g.s_bk + g.N + tb) * 4 >= (1LL << 31) ||
+        nt > 0x7FFFFFFF)
+        return p;
+    p.nb = nb, p.ks = ks, p.tiles = nt;
+    return p;
+}
+
+template <int NB, int KS>
+static void launch_split_ks(const GemmArgs &g, bool avec, unsigned nwg, hipStream_t st) {
+    if (avec) PITON_LAUNCH((gemm_split_kernel<NB, KS, true>), dim3(nwg), dim3(64 * KS), 0, st, g);
+    else PITON_LAUNCH((gemm_split_kernel<NB, KS, false>), dim3(nwg), dim3(64 * KS), 0, st, g);
+}
+
+template <int NB>
+static void launch_split_nb(const GemmArgs &g, int ks, bool avec, unsigned nwg, hipStream_t st) {
+    if (ks == 1) launch_split_ks<NB, 1>(g, avec, nwg, st);
+    else if (ks == 2) launch_split_ks<NB, 2>(g, avec, nwg, st);
+    else launch_split_ks<NB, 4>(g, avec, nwg, st);
+}
+
 template <int A_L>
 static void launch_b(int bl, const GemmArgs &g, int nwg, hipStream_t st) {
     if (bl == VEC_ROW) PITON_LAUNCH((gemm_f32_kernel<A_L, VEC_ROW, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
@@ -614,12 +801,16 @@ static void launch_b(int bl, const GemmArgs &g, int nwg, hipStream_t st) {
     else PITON_LAUNCH((gemm_f32_kernel<A_L, SCALAR, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
 }
 
-static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
+// split_ok: row-major shapes that give the direct kernel fewer 128 x 128 tiles than CUs, or
+// that are not whole tiles, take the split kernel (its k order differs from the LDS kernel's, so
+// the dense entry, whose bits the fused digits chain reproduces, keeps the LDS kernel)
+static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_ok) {
     if (g.M == 0 || g.N == 0) return PITON_OK;
     const int64_t tiles = ((g.M + GBM - 1) / GBM) * ((g.N + GBN - 1) / GBN);
     PITON_REQUIRE(tiles <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "%s: %lld tiles exceed one grid", what, (long long)tiles);
     // a group taller than the tile rows orders tiles exactly as a group of all of them does;
     // the clamp keeps group_m * num_pid_n within the tile count (no 32-bit overflow in the kernels)
+    const int group_user = g.group_m;
     const int64_t num_pid_m = (g.M + GBM - 1) / GBM;
     if (g.group_m > num_pid_m) g.group_m = (int)num_pid_m;
     g.a_kfast = llabs(g.s_ak) <= llabs(g.s_am);
@@ -629,8 +820,20 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what) {
     const bool whole = al == VEC_ROW && bl == VEC_ROW && g.M % GBM == 0 && g.N % GBN == 0 && g.K % GBK == 0 && g.K > 0;
     // the direct kernel addresses rows by 32-bit byte offsets from the matrix base: positive row
     // strides and every element within 2^31 bytes
-    if (PITON_GEMM_DIRECT && whole && g.M % DBM == 0 && g.N % DBN == 0 && g.K % (2 * DKT) == 0 && g.s_am > 0 &&
-        g.s_bk > 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) && (g.K - 1) * g.s_bk + g.N < (1LL << 29))
+    const bool direct = PITON_GEMM_DIRECT && whole && g.M % DBM == 0 && g.N % DBN == 0 && g.K % (2 * DKT) == 0 &&
+                        g.s_am > 0 && g.s_bk > 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) &&
+                        (g.K - 1) * g.s_bk + g.N < (1LL << 29);
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const SplitPlan sp = split_ok && !(direct && tiles >= cus) ? plan_split(g, cus) : SplitPlan{0, 0, 0};
+    if (sp.nb > 0) {
+        // the split kernel's group order runs over its own tile rows
+        const int64_t rows = (g.M + 32 * sp.nb - 1) / (32 * sp.nb);
+        GemmArgs gs = g;
+        gs.group_m = (int)(group_user > rows ? rows : group_user);
+        const bool avec = g.s_am % 4 == 0 && g.K % 4 == 0 && aligned16(g.a);
+        if (sp.nb == 2) launch_split_nb<2>(gs, sp.ks, avec, (unsigned)sp.tiles, st);
+        else launch_split_nb<1>(gs, sp.ks, avec, (unsigned)sp.tiles, st);
+    } else if (direct)
         PITON_LAUNCH(gemm_direct_kernel, dim3((unsigned)((g.M / DBM) * (g.N / DBN))), dim3(GTHREADS), 0, st, g);
     else if (whole)
         PITON_LAUNCH((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);
@@ -658,7 +861,7 @@ int32_t piton_mi355x_matmul(const float *a, const float *b, float *c, int64_t M,
     if (rc) return rc;
     GemmArgs g{a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn,
                group_size_m, nullptr, 0, nullptr, 0, 0, 0};
-    rc = launch_gemm(g, (hipStream_t)stream, "matmul");
+    rc = launch_gemm(g, (hipStream_t)stream, "matmul", true);
     if (rc == PITON_OK) clear_error();
     return rc;
 }
@@ -679,7 +882,7 @@ int32_t piton_mi355x_dense(const float *x, const float *w, const float *bias, fl
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     GemmArgs g{x, w, y, M, N, K, K, 1, N, 1, N, 1, 1, add_bias ? bias : nullptr, relu ? 1 : 0, nullptr, 0, 0, 0};
-    rc = launch_gemm(g, st, "dense");
+    rc = launch_gemm(g, st, "dense", false);
     if (rc) return rc;
     if (argmax_out && M > 0) {
         PITON_REQUIRE((M + 3) / 4 <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "dense: M=%lld too large", (long long)M);
@@ -716,7 +919,7 @@ int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *w, const f
             PITON_LAUNCH((gemm_small_m_kernel<false, false>), grid, block, 0, (hipStream_t)stream, g);
         rc = check_launch("linear");
     } else {
-        rc = launch_gemm(g, (hipStream_t)stream, "linear");
+        rc = launch_gemm(g, (hipStream_t)stream, "linear", true);
     }
     if (rc == PITON_OK) clear_error();
     return rc;

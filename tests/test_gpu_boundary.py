@@ -24,16 +24,17 @@ def test_matmul_numpy_through_the_reference_call():
                                  1, N, 1, BLOCK_SIZE_M=8, BLOCK_SIZE_N=64, BLOCK_SIZE_K=8, GROUP_SIZE_M=8)
     np.testing.assert_array_equal(c, oracle.matmul(a, b))
     (launch,) = rec.last_stats["launches"]
-    assert launch["kernel"].startswith("gemm_f32_kernel") and launch["block"] == (256, 1, 1)
-    assert launch["grid"][0] == cdiv(M, 128) * cdiv(N, 128) and launch["vgprs"] > 0
-    assert launch["lds_bytes"] > 0 and launch["scratch_bytes"] == 0
+    # a product this small takes the split kernel: 32 x 32 tiles, waves splitting K
+    assert launch["kernel"].startswith("gemm_split_kernel") and launch["grid"][0] == cdiv(M, 32) * cdiv(N, 32)
+    assert launch["block"][0] in (64, 128, 256) and launch["vgprs"] > 0 and launch["scratch_bytes"] == 0
     assert rec.last_stats["flops"] == 2 * M * N * K
 
 
 def test_matmul_tensors_whole_tiles_take_the_direct_kernel(monkeypatch):
+    """2048^3 has as many 128 x 128 tiles as the chip has CUs: the register-direct kernel."""
     monkeypatch.setenv("PITON_MI355X_TIMING", "1")
     g = torch.Generator(device="cuda").manual_seed(3)
-    n = 512
+    n = 2048
     a = torch.rand((n, n), device="cuda", generator=g)
     b = torch.rand((n, n), device="cuda", generator=g)
     c = torch.empty((n, n), device="cuda")

@@ -236,3 +236,56 @@ def test_out_of_storage_strides_are_rejected():
     a = torch.zeros((8, 8), device="cuda")
     with pytest.raises(ValueError):
         rt.matmul(a, a, a, 8, 8, 9, 8, 1, 8, 1, 8, 1)
+
+
+# shapes that give the register-direct kernel fewer 128 x 128 tiles than CUs, or ragged edges:
+# the split kernel (64 x 64 or 32 x 32 workgroup tiles, waves splitting K)
+SPLIT_SHAPES = [(512, 512, 512, 0, 0), (1024, 1024, 1024, 0, 0), (1000, 1800, 700, 3, 5), (1000, 1800, 700, 4, 8),
+                (130, 70, 33, 0, 0), (2048, 768, 256, 0, 0), (77, 300, 1, 0, 0), (300, 1, 5000, 0, 0),
+                (257, 129, 97, 1, 2)]
+
+
+@pytest.mark.parametrize("M,N,K,pad_a,pad_b", SPLIT_SHAPES)
+def test_split_kernel_dyadic_with_nan_padding(M, N, K, pad_a, pad_b):
+    """Dyadic inputs (every product and sum exact: any order gives the same bits) with NaN in
+    the row padding of A and B: the K tail of A and the columns of B past N never reach a
+    stored element, and C's padding (a guard band) stays untouched."""
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    a, b = dyadic(rng, (M, K)), dyadic(rng, (K, N))
+    A = torch.full((M, K + pad_a), float("nan"), device="cuda")
+    B = torch.full((K, N + pad_b), float("nan"), device="cuda")
+    A[:, :K] = torch.from_numpy(a).cuda()
+    B[:, :N] = torch.from_numpy(b).cuda()
+    C = torch.full((M + 1, N + 3), -7.0, device="cuda")
+    rt.matmul(A, B, C, M, N, K, K + pad_a, 1, N + pad_b, 1, N + 3, 1, 8)
+    (launch,) = rt.last_launches()
+    torch.cuda.synchronize()
+    got = C.cpu().numpy()
+    np.testing.assert_array_equal(got[:M, :N], a @ b)
+    assert (got[M:] == -7.0).all() and (got[:, N:] == -7.0).all()
+    assert launch["kernel"].startswith("gemm_split_kernel"), launch
+    assert launch["block"][0] in (64, 128, 256) and launch["scratch_bytes"] == 0
+
+
+@pytest.mark.parametrize("M,N,K,pad_a,pad_b", SPLIT_SHAPES[:4])
+def test_split_kernel_uniform_against_float64_and_oracle(M, N, K, pad_a, pad_b):
+    rng = np.random.default_rng(K)
+    a = rng.uniform(-1, 1, (M, K + pad_a)).astype(np.float32)
+    b = rng.uniform(-1, 1, (K, N + pad_b)).astype(np.float32)
+    C = torch.empty((M, N), device="cuda")
+    rt.matmul(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), C, M, N, K, K + pad_a, 1, N + pad_b, 1, N, 1, 8)
+    got = C.cpu().numpy()
+    ref = fp64.matmul(a[:, :K], b[:, :N])
+    assert fp64.rel_fro(got, ref) <= TOL
+    rows = np.random.default_rng(0).choice(M, 64, replace=False)
+    emu = oracle.matmul_fast(np.ascontiguousarray(a[rows, :K]), np.ascontiguousarray(b[:, :N]), threads=8)
+    assert fp64.rel_fro(got[rows], ref[rows]) <= fp64.rel_fro(emu, ref[rows])
+
+
+def test_split_kernel_group_order_and_repeatability():
+    g = torch.Generator(device="cuda").manual_seed(21)
+    a = torch.rand((1000, 700), device="cuda", generator=g)
+    b = torch.rand((700, 1800), device="cuda", generator=g)
+    base = run(a, b, group=8)
+    for group in (1, 5, 2 ** 31 - 1, 8):
+        assert torch.equal(run(a, b, group=group), base)

@@ -451,14 +451,25 @@ void gemm_direct_kernel(GemmArgs g) {
 // does. The KS partial tiles meet in LDS and add in wave order (fixed: the result does not
 // depend on timing); the epilogue (bias, ReLU, residual) then stores rows < M and columns < N.
 // AVEC: A rows 16-byte aligned (16-byte loads of A); otherwise 4-byte loads.
-constexpr int kMaxSplitWaves = 4;
+#ifndef PITON_SPLIT_MAX_WAVES
+#define PITON_SPLIT_MAX_WAVES 4
+#endif
+#ifndef PITON_SPLIT_WAVES_PER_CU
+#define PITON_SPLIT_WAVES_PER_CU 4
+#endif
+// the direct kernel takes whole-tile shapes with at least this many 128 x 128 tiles per CU
+#ifndef PITON_DIRECT_TILES_PER_CU
+#define PITON_DIRECT_TILES_PER_CU 1
+#endif
+constexpr int kMaxSplitWaves = PITON_SPLIT_MAX_WAVES;
 
 template <int NB, int KS, bool AVEC>
 __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     constexpr int TB = 32 * NB;
     constexpr int NACC = NB * NB * 16;  // accumulator registers per lane
     __shared__ float red[KS > 1 ? KS : 1][NACC][64];
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    // the wave index is uniform: readfirstlane makes the K loop, which starts at it, a scalar loop
+    const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
     const int half = lane >> 5, l31 = lane & 31;
 
     const int num_pid_m = (int)((g.M + TB - 1) / TB);
@@ -484,29 +495,35 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     for (int j = 0; j < NB; j++) vb[j] = (uint32_t)(((int64_t)(16 * half) * g.s_bk + n0 + j * 32 + l31) * 4);
     const uint32_t sbk4 = (uint32_t)(g.s_bk * 4);
     const int nk = (int)((g.K + 31) / 32);
-    const int k_tail = (int)(g.K - (int64_t)(nk - 1) * 32);  // valid k of the last tile, 1..32
 
     struct Ops {
         float a[NB][16];
         float b[NB][16];
     };
-    // every offset goes in the per-lane address, which is what the descriptor's range check covers
+    // every offset goes in the per-lane address, which is what the descriptor's range check
+    // covers. The K tail: a lane's A elements with k >= K get an offset past the bound (2^31,
+    // beyond any bound of a matrix under 2 GiB), so they read as zero with no data dependence;
+    // B's rows past K are past its bound already.
+    constexpr uint32_t kOut = 0x80000000u;
     auto load = [&](int kt, Ops &o) {
         const uint32_t ka = (uint32_t)kt * 128u, kb = (uint32_t)kt * 32u * sbk4;
+        const int64_t k0 = (int64_t)kt * 32 + 16 * half;  // this lane's first k of the tile
 #pragma unroll
         for (int i = 0; i < NB; i++) {
             if constexpr (AVEC) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const f32x4 v = __builtin_bit_cast(
-                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(va[i] + ka + 16 * q), 0, 0));
+                    const uint32_t off = k0 + 4 * q < g.K ? va[i] + ka + 16 * q : kOut;
+                    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0));
 #pragma unroll
                     for (int e = 0; e < 4; e++) o.a[i][4 * q + e] = v[e];
                 }
             } else {
 #pragma unroll
-                for (int s = 0; s < 16; s++)
-                    o.a[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)(va[i] + ka + 4 * s), 0, 0));
+                for (int s = 0; s < 16; s++) {
+                    const uint32_t off = k0 + s < g.K ? va[i] + ka + 4 * s : kOut;
+                    o.a[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)off, 0, 0));
+                }
             }
         }
 #pragma unroll
@@ -522,15 +539,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
         for (int j = 0; j < NB; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-    auto mul = [&](Ops &o, int kt) {
-        if (kt == nk - 1 && k_tail < 32) {
-            // the K tail: this lane's k = 16 half + s past K contributes nothing
-#pragma unroll
-            for (int s = 0; s < 16; s++)
-                if (16 * half + s >= k_tail)
-#pragma unroll
-                    for (int i = 0; i < NB; i++) o.a[i][s] = 0.f;
-        }
+    auto mul = [&](const Ops &o) {
 #pragma unroll
         for (int s = 0; s < 16; s++)
 #pragma unroll
@@ -540,16 +549,39 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i][s], o.b[j][s], acc[i][j], 0, 0, 0);
     };
     // this wave's K tiles: wave, wave + KS, ...; the next one is in flight while one multiplies.
-    // The prefetch past the last tile reads at or beyond the descriptors' bounds (zeros) or
-    // inside the matrices, and is never used.
+    // Tiles come in pairs with no condition between loads and products (a conditional product
+    // lets the compiler sink its loads next to it, ending the prefetch): a tile past the last
+    // one reads zeros for A (k >= K) and B (rows past K) and adds exact zeros; the prefetch
+    // after the last pair is never used.
+    // The scheduling barriers keep each tile's loads together ahead of the other tile's products
+    // (left free, the scheduler moves every load next to its first use to save registers).
+    // Each half-step issues the next tile's loads between this tile's products, PITON_SPLIT_LPM
+    // loads after each MFMA from the first one on (a wave alone on its SIMD otherwise stops the
+    // matrix pipe while it issues a tile's worth of loads), and the scheduling barriers keep the
+    // halves apart. One load per MFMA measured best (1024^3: 22.3 us; two 23.0, three 23.8; all
+    // loads ahead of the products 27.6).
+#ifndef PITON_SPLIT_LPM
+#define PITON_SPLIT_LPM 1
+#endif
+    constexpr int LOADS = NB * (AVEC ? 4 : 16) + NB * 16, MFMAS = 16 * NB * NB, LPM = PITON_SPLIT_LPM;
+    auto interleave = [&]() {
+#pragma unroll
+        for (int i = 0; i < MFMAS; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            if (i * LPM < LOADS) __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);  // LPM VMEM reads
+        }
+    };
     Ops o0, o1;
     load(wave, o0);
     for (int kt = wave; kt < nk; kt += 2 * KS) {
         load(kt + KS, o1);
-        mul(o0, kt);
-        if (kt + KS >= nk) break;
+        mul(o0);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
         load(kt + 2 * KS, o0);
-        mul(o1, kt + KS);
+        mul(o1);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // accumulator r of a 32x32 block holds row 8*(r/4) + 4*half + r%4, column l31
@@ -768,10 +800,13 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     if (g.s_ak != 1 || g.s_bn != 1 || g.s_am <= 0 || g.s_bk <= 0 || g.K <= 0 || g.M <= 0 || g.N <= 0) return p;
     auto tiles = [&](int64_t tb) { return ((g.M + tb - 1) / tb) * ((g.N + tb - 1) / tb); };
     const int64_t nk = (g.K + 31) / 32;
-    const int nb = tiles(64) >= cus ? 2 : 1;
+#ifndef PITON_SPLIT_NB_MAX
+#define PITON_SPLIT_NB_MAX 2
+#endif
+    const int nb = PITON_SPLIT_NB_MAX > 1 && tiles(64) >= cus ? 2 : 1;
     const int64_t nt = tiles(32 * nb);
     int ks = 1;
-    while (ks < kMaxSplitWaves && nt * ks < 4 * (int64_t)cus && 4 * ks <= nk) ks *= 2;
+    while (ks < kMaxSplitWaves && nt * ks < PITON_SPLIT_WAVES_PER_CU * (int64_t)cus && 4 * ks <= nk) ks *= 2;
     // every byte offset a lane forms (the prefetch past the last tile included) stays below 2^31
     const int64_t tb = 32 * nb, kpad = g.K + 32 * (2 * ks + 3);  // the farthest prefetch: tile nk - 1 + 2 ks
     if (((g.M + tb) * g.s_am + kpad) * 4 >= (1LL << 31) || (kpad * g.s_bk + g.N + tb) * 4 >= (1LL << 31) ||
@@ -791,6 +826,9 @@ template <int NB>
 static void launch_split_nb(const GemmArgs &g, int ks, bool avec, unsigned nwg, hipStream_t st) {
     if (ks == 1) launch_split_ks<NB, 1>(g, avec, nwg, st);
     else if (ks == 2) launch_split_ks<NB, 2>(g, avec, nwg, st);
+#if PITON_SPLIT_MAX_WAVES > 4
+    else if (ks == 8) launch_split_ks<NB, 8>(g, avec, nwg, st);
+#endif
     else launch_split_ks<NB, 4>(g, avec, nwg, st);
 }
 
@@ -824,7 +862,8 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
                         g.s_am > 0 && g.s_bk > 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) &&
                         (g.K - 1) * g.s_bk + g.N < (1LL << 29);
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-    const SplitPlan sp = split_ok && !(direct && tiles >= cus) ? plan_split(g, cus) : SplitPlan{0, 0, 0};
+    const SplitPlan sp =
+        split_ok && !(direct && tiles >= PITON_DIRECT_TILES_PER_CU * cus) ? plan_split(g, cus) : SplitPlan{0, 0, 0};
     if (sp.nb > 0) {
         // the split kernel's group order runs over its own tile rows
         const int64_t rows = (g.M + 32 * sp.nb - 1) / (32 * sp.nb);

@@ -342,7 +342,12 @@ constexpr int DKH = DKT / 2;               // k per lane half per tile
 // TFLOP/s; 4 x 2 and 2 x 4 at 292-296 VGPRs, one wave per SIMD: 137 and 134)
 constexpr int DMB = PITON_GEMM_DIRECT_MB, DNB = PITON_GEMM_DIRECT_NB;
 constexpr int DBM = 64 * DMB, DBN = 64 * DNB;                           // workgroup tile (2 x 2 waves)
-__global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(PITON_GEMM_DIRECT_WAVES)))
+// ONE_GEN: the launch has at most one workgroup per CU (a wave alone on its SIMD): the next
+// tile's loads are interleaved with this tile's products, one after each MFMA, as in the split
+// kernel (2048^3: 163 -> 141 us). With several workgroups per CU the other waves hide the loads
+// and the interleave only slows the wave down (4096^3: 1.02 -> 1.42 ms), so it is off there.
+template <bool ONE_GEN>
+__global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(ONE_GEN ? 2 : PITON_GEMM_DIRECT_WAVES)))
 void gemm_direct_kernel(GemmArgs g) {
     const int t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63;
@@ -411,13 +416,26 @@ void gemm_direct_kernel(GemmArgs g) {
     // also keeps the uniform offsets in `soffset` legal (the descriptor's range check covers the
     // per-lane offset only)
     const int nk = (int)(g.K / DKT);
+    constexpr int DLOADS = DMB * DKH / 4 + DNB * DKH, DMFMAS = DKH * DMB * DNB;
+    auto interleave = [&]() {
+        if constexpr (ONE_GEN) {
+#pragma unroll
+            for (int i = 0; i < DMFMAS; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
+                if (i < DLOADS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one VMEM read
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     Ops o0, o1;
     load(0, o0);
     for (int kt = 0; kt < nk; kt += 2) {
         load(kt + 1, o1);
         mul(o0);
+        interleave();
         load(min(kt + 2, nk - 1), o0);
         mul(o1);
+        interleave();
     }
 
     // accumulator r of a 32x32 block holds row 8*(r/4) + 4*half + r%4, column l31
@@ -455,7 +473,7 @@ void gemm_direct_kernel(GemmArgs g) {
 #define PITON_SPLIT_MAX_WAVES 4
 #endif
 #ifndef PITON_SPLIT_WAVES_PER_CU
-#define PITON_SPLIT_WAVES_PER_CU 4
+#define PITON_SPLIT_WAVES_PER_CU 8
 #endif
 // the direct kernel takes whole-tile shapes with at least this many 128 x 128 tiles per CU
 #ifndef PITON_DIRECT_TILES_PER_CU
@@ -789,8 +807,9 @@ static int layout_b(const GemmArgs &g) {
 
 // The split kernel's tile (NB blocks of 32 per side) and waves per workgroup for a row-major
 // shape, or nb = 0 when it does not apply. Tiles of 64 when there are at least as many as
-// CUs, else of 32; then the waves double (up to kMaxSplitWaves) until the launch has four
-// waves per CU, as long as each wave keeps at least two K tiles.
+// CUs, else of 32; then the waves double (up to kMaxSplitWaves) until the launch has
+// PITON_SPLIT_WAVES_PER_CU waves per CU, as long as each wave keeps at least two K tiles
+// (8 per CU: 1536^3 103 -> 88 us against 4; the other shapes measured the same).
 struct SplitPlan {
     int nb, ks;
     int64_t tiles;
@@ -872,9 +891,11 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
         const bool avec = g.s_am % 4 == 0 && g.K % 4 == 0 && aligned16(g.a);
         if (sp.nb == 2) launch_split_nb<2>(gs, sp.ks, avec, (unsigned)sp.tiles, st);
         else launch_split_nb<1>(gs, sp.ks, avec, (unsigned)sp.tiles, st);
-    } else if (direct)
-        PITON_LAUNCH(gemm_direct_kernel, dim3((unsigned)((g.M / DBM) * (g.N / DBN))), dim3(GTHREADS), 0, st, g);
-    else if (whole)
+    } else if (direct && tiles <= cus) {
+        PITON_LAUNCH(gemm_direct_kernel<true>, dim3((unsigned)tiles), dim3(GTHREADS), 0, st, g);
+    } else if (direct) {
+        PITON_LAUNCH(gemm_direct_kernel<false>, dim3((unsigned)tiles), dim3(GTHREADS), 0, st, g);
+    } else if (whole)
         PITON_LAUNCH((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);
     else if (al == VEC_ROW) launch_b<VEC_ROW>(bl, g, nwg, st);
     else if (al == VEC_COL) launch_b<VEC_COL>(bl, g, nwg, st);

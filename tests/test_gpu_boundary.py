@@ -41,7 +41,7 @@ def test_matmul_tensors_whole_tiles_take_the_direct_kernel(monkeypatch):
     rec = patched_reference_call(RefJIT(ref_matmul_kernel), (cdiv(n, 128) ** 2,), a, b, c, n, n, n, n, 1, n, 1, n,
                                  1, BLOCK_SIZE_M=128, BLOCK_SIZE_N=128, BLOCK_SIZE_K=32, GROUP_SIZE_M=8)
     torch.cuda.synchronize()
-    assert rec.last_stats["launches"][0]["kernel"] == "gemm_direct_kernel"
+    assert rec.last_stats["launches"][0]["kernel"].startswith("gemm_direct_kernel")
     assert rec.last_stats["elapsed_us"] > 0
     ref = fp64.matmul(a.cpu().numpy(), b.cpu().numpy())
     assert fp64.rel_fro(c.cpu().numpy(), ref) <= 1e-5

@@ -468,7 +468,10 @@ void gemm_direct_kernel(GemmArgs g) {
 // may hold padding or the next row) is zeroed before its products, as the reference's K mask
 // does. The KS partial tiles meet in LDS and add in wave order (fixed: the result does not
 // depend on timing); the epilogue (bias, ReLU, residual) then stores rows < M and columns < N.
-// AVEC: A rows 16-byte aligned (16-byte loads of A); otherwise 4-byte loads.
+// AVEC: A rows 16-byte aligned (16-byte loads of A). Otherwise each lane's 16 consecutive A
+// values sit r = (row start) mod 4 floats past a 16-byte boundary, the same r for every K tile:
+// the lane loads the five aligned 16-byte chunks that cover them and picks the four-way shift in
+// registers (5 loads and about 50 selects per block instead of 16 loads).
 #ifndef PITON_SPLIT_MAX_WAVES
 #define PITON_SPLIT_MAX_WAVES 4
 #endif
@@ -501,21 +504,33 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     const int pid_n = (pid % in_group) / gsize;
     const int64_t m0 = (int64_t)pid_m * TB, n0 = (int64_t)pid_n * TB;
 
-    // bounded at the last element of each matrix: offsets at or past the bound read as zero
-    const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.a), (short)0,
-                                                      (int)(((g.M - 1) * g.s_am + g.K) * 4), 0x00020000);
+    // bounded at the last element of each matrix: offsets at or past the bound read as zero. A's
+    // descriptor starts at the 16-byte boundary at or below A (inside A's allocation, whose start
+    // is aligned) and its bound is rounded up to whole 16-byte chunks (the last chunk lies in the
+    // page of A's last element), so a 16-byte load is either wholly inside or wholly outside.
+    const int off0 = (int)((reinterpret_cast<uintptr_t>(g.a) >> 2) & 3);  // A's first float past the boundary
+    const float *a_al = g.a - off0;
+    const int64_t a_end = off0 + (g.M - 1) * g.s_am + g.K;                  // floats from a_al
+    const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a_al), (short)0,
+                                                      (int)(((a_end + 3) & ~(int64_t)3) * 4), 0x00020000);
     const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.b), (short)0,
                                                       (int)(((g.K - 1) * g.s_bk + g.N) * 4), 0x00020000);
     uint32_t va[NB], vb[NB];
+    int ra_shift[NB];  // !AVEC: this lane's row start past its 16-byte boundary, in floats
 #pragma unroll
-    for (int i = 0; i < NB; i++) va[i] = (uint32_t)(((m0 + i * 32 + l31) * g.s_am + 16 * half) * 4);
+    for (int i = 0; i < NB; i++) {
+        const int64_t e0 = off0 + (m0 + i * 32 + l31) * g.s_am + 16 * half;
+        ra_shift[i] = (int)(e0 & 3);
+        va[i] = (uint32_t)((e0 & ~(int64_t)3) * 4);
+    }
 #pragma unroll
     for (int j = 0; j < NB; j++) vb[j] = (uint32_t)(((int64_t)(16 * half) * g.s_bk + n0 + j * 32 + l31) * 4);
     const uint32_t sbk4 = (uint32_t)(g.s_bk * 4);
     const int nk = (int)((g.K + 31) / 32);
 
+    constexpr int AW = AVEC ? 16 : 20;  // A floats a lane loads per block and tile
     struct Ops {
-        float a[NB][16];
+        float a[NB][AW];
         float b[NB][16];
     };
     // every offset goes in the per-lane address, which is what the descriptor's range check
@@ -537,10 +552,13 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
                     for (int e = 0; e < 4; e++) o.a[i][4 * q + e] = v[e];
                 }
             } else {
+                // the chunks holding k0 - r .. k0 - r + 19; the K tail is zeroed in mul
 #pragma unroll
-                for (int s = 0; s < 16; s++) {
-                    const uint32_t off = k0 + s < g.K ? va[i] + ka + 4 * s : kOut;
-                    o.a[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)off, 0, 0));
+                for (int q = 0; q < 5; q++) {
+                    const uint32_t off = k0 - ra_shift[i] + 4 * q < g.K ? va[i] + ka + 16 * q : kOut;
+                    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o.a[i][4 * q + e] = v[e];
                 }
             }
         }
@@ -557,14 +575,41 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
         for (int j = 0; j < NB; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-    auto mul = [&](const Ops &o) {
+    // !AVEC: the lane's 16 values of block i: window[s + r], zero where k0 + s >= K
+    auto a_vals = [&](const Ops &o, int i, int kt, float (&v)[16]) {
+        if constexpr (AVEC) {
+#pragma unroll
+            for (int s = 0; s < 16; s++) v[s] = o.a[i][s];
+        } else {
+            // bitwise blends with all-ones / all-zero masks (v_bfi): a select between two array
+            // elements becomes a dynamic index, which moves the array to scratch memory
+            const int r = ra_shift[i];
+            const int64_t nvalid = g.K - ((int64_t)kt * 32 + 16 * half);
+            const uint32_t m1 = 0u - (uint32_t)(r & 1), m2 = 0u - (uint32_t)((r >> 1) & 1);
+            uint32_t t0[18];
+#pragma unroll
+            for (int s = 0; s < 18; s++) {
+                const uint32_t x0 = __float_as_uint(o.a[i][s]), x1 = __float_as_uint(o.a[i][s + 1]);
+                t0[s] = x0 ^ ((x0 ^ x1) & m1);
+            }
+#pragma unroll
+            for (int s = 0; s < 16; s++) {
+                const uint32_t x = t0[s] ^ ((t0[s] ^ t0[s + 2]) & m2);
+                v[s] = __uint_as_float(x & (0u - (uint32_t)(s < nvalid)));
+            }
+        }
+    };
+    auto mul = [&](const Ops &o, int kt) {
+        float av[NB][16];
+#pragma unroll
+        for (int i = 0; i < NB; i++) a_vals(o, i, kt, av[i]);
 #pragma unroll
         for (int s = 0; s < 16; s++)
 #pragma unroll
             for (int i = 0; i < NB; i++)
 #pragma unroll
                 for (int j = 0; j < NB; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i][s], o.b[j][s], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], o.b[j][s], acc[i][j], 0, 0, 0);
     };
     // this wave's K tiles: wave, wave + KS, ...; the next one is in flight while one multiplies.
     // Tiles come in pairs with no condition between loads and products (a conditional product
@@ -581,7 +626,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
 #ifndef PITON_SPLIT_LPM
 #define PITON_SPLIT_LPM 1
 #endif
-    constexpr int LOADS = NB * (AVEC ? 4 : 16) + NB * 16, MFMAS = 16 * NB * NB, LPM = PITON_SPLIT_LPM;
+    constexpr int LOADS = NB * (AVEC ? 4 : 5) + NB * 16, MFMAS = 16 * NB * NB, LPM = PITON_SPLIT_LPM;
     auto interleave = [&]() {
 #pragma unroll
         for (int i = 0; i < MFMAS; i++) {
@@ -593,11 +638,11 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     load(wave, o0);
     for (int kt = wave; kt < nk; kt += 2 * KS) {
         load(kt + KS, o1);
-        mul(o0);
+        mul(o0, kt);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
         load(kt + 2 * KS, o0);
-        mul(o1);
+        mul(o1, kt + KS);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
     }

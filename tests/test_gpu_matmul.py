@@ -289,3 +289,23 @@ def test_split_kernel_group_order_and_repeatability():
     base = run(a, b, group=8)
     for group in (1, 5, 2 ** 31 - 1, 8):
         assert torch.equal(run(a, b, group=group), base)
+
+
+@pytest.mark.parametrize("a_off,lda", [(1, 700), (2, 703), (3, 701), (1, 64)])
+def test_split_kernel_unaligned_base_and_rows(a_off, lda):
+    """A starting 1-3 floats past a 16-byte boundary, rows of any length: each lane reads the
+    aligned 16-byte chunks around its values and selects them in registers; dyadic inputs give
+    numpy's bits, with NaN before A, between its rows and after it."""
+    M, N, K = 333, 200, min(lda, 77 if lda == 64 else 650)
+    rng = np.random.default_rng(a_off * 1000 + lda)
+    a, b = dyadic(rng, (M, K)), dyadic(rng, (K, N))
+    store = torch.full((a_off + M * lda + 8,), float("nan"), device="cuda")
+    A = store[a_off:a_off + M * lda].view(M, lda)
+    A[:, :K] = torch.from_numpy(a).cuda()
+    B = torch.from_numpy(b).cuda()
+    C = torch.full((M, N), -7.0, device="cuda")
+    rt.matmul(A, B, C, M, N, K, lda, 1, N, 1, N, 1, 8)
+    (launch,) = rt.last_launches()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(C.cpu().numpy(), a @ b)
+    assert launch["kernel"] == "gemm_split_kernel<NB, KS, false>"

@@ -254,16 +254,30 @@ def bench_softmax(n, rows=4096, launches=48, sample_rows=256):
     # the copy ceiling of the same traffic: this library's copy (16-byte nontemporal loads and
     # stores, one vector per thread) over the same rotated buffers
     copy = timed_graph(lambda i: rt.copy(xs[i % pairs], ys[i % pairs], rows * n), max(launches, pairs))
+    # the two halves of the traffic apart: a read-only pass over the inputs (this library's row
+    # sum over the same bytes seen as n rows of 4096 aligned floats: reads every float, writes
+    # one per row) and a write-only pass over the outputs (torch's fill), plus an empty graph
+    # node (a one-float copy) for the per-launch cost
+    sums = torch.empty(max(rows, n), device="cuda")
+    read = timed_graph(lambda i: rt.row_sum(xs[i % pairs].view(n, rows), sums, n, rows, rows), max(launches, pairs))
+    write = timed_graph(lambda i: ys[i % pairs].fill_(0.5), max(launches, pairs))
+    one = torch.zeros(1, device="cuda")
+    node = timed_graph(lambda i: rt.copy(one, sums, 1), launches)
     step(0)
     torch.cuda.synchronize()
     # the special rows and a strided sample of the others
     idx = torch.cat([torch.arange(1, 4), torch.arange(0, rows, rows // sample_rows)]).cuda()
     sample = (xs[0][idx].cpu().numpy(), ys[0][idx].cpu().numpy())
-    del xs, ys
+    del xs, ys, sums, one
     torch.cuda.empty_cache()
+    half = pair_bytes // 2
     line = dict(n=n, rows=rows, kernel=kernel, bytes=pair_bytes, us=round(avg * 1e6, 3),
                 gbs=round(pair_bytes / avg / 1e9, 1), frac=round(pair_bytes / avg / PEAK_HBM, 4),
-                copy_gbs=round(pair_bytes / copy / 1e9, 1), traffic=measured_traffic(f"softmax {rows} x {n}"))
+                copy_gbs=round(pair_bytes / copy / 1e9, 1), traffic=measured_traffic(f"softmax {rows} x {n}"),
+                bound=dict(read_us=round(read * 1e6, 3), read_gbs=round(half / read / 1e9, 1),
+                           write_us=round(write * 1e6, 3), write_gbs=round(half / write / 1e9, 1),
+                           two_pass_us=round((read + write) * 1e6, 3), node_us=round(node * 1e6, 3),
+                           frac_of_two_pass=round((read + write) / avg, 4)))
     return line, sample
 
 

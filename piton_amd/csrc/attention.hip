@@ -99,6 +99,19 @@ __device__ __forceinline__ void map_group(const AttnArgs &g, int64_t &bh, int &q
     qg = g.causal ? nqg - 1 - qrank : qrank;
 }
 
+// The key blocks of a query group are dealt to the ANW waves round-robin, wave w taking blocks
+// first_block(w, qg), + ANW, ... Groups qg = 2 (mod 4) start one wave later. A causal group has
+// qg + 1 blocks, so its one to three blocks past a multiple of ANW land on waves {0} (qg = 0),
+// {0, 1} (qg = 1) and {1, 2, 3} (qg = 2), qg taken mod 4: the two groups of a causal pair (qg + qg' =
+// nqg - 1) then leave exactly one wave with a block more than the others, where dealing every
+// group from wave 0 gives two waves one more and one wave one less whenever the pair's groups
+// are 1 and 2 (mod 4). The rule depends on the group alone, so a query's keys are split among
+// the waves the same way whatever n_ctx is (causal prefixes stay bit-identical).
+static_assert((ANW & (ANW - 1)) == 0, "ANW a power of two");
+__device__ __forceinline__ int first_block(int wave, int qg) {
+    return (wave - (qg % 4 == 2 ? 1 : 0)) & (ANW - 1);
+}
+
 // S^T = K Q'^T for one block of 32 keys: lane (half, l31) gets 16 scores of query l31, register r
 // holding key 8*(r/4) + 4*half + r%4 of the block
 template <int D>
@@ -109,6 +122,19 @@ __device__ __forceinline__ f32x16 block_scores(const float (&kf)[D / 2], const f
 #pragma unroll
     for (int s = 0; s < D / 2; s++) st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[s], st, 0, 0, 0);
     return st;
+}
+
+// The two halves of a wave hold the two halves of a query's keys. v_permlane32_swap of a value
+// with itself leaves the low half's values in every lane of one result and the high half's in
+// every lane of the other: a VALU exchange, no LDS round trip. max and + are commutative, so
+// every lane gets the value of the lane-order expression max(x, x^32) / x + x^32.
+__device__ __forceinline__ float halves_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // keys past n_ctx, and under causal masking keys after the query, score -inf; only blocks that
@@ -136,8 +162,8 @@ __device__ __forceinline__ float online_rescale(const f32x16 &st, float &m_i, fl
     float mloc = st[0];
 #pragma unroll
     for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, st[r]);
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));  // the other half of the wave holds the query's other keys
-    const bool move = mloc > m_i + kSlack;     // m_i = -inf: moves on the first visible score
+    mloc = halves_max(mloc);                // the other half of the wave holds the query's other keys
+    const bool move = mloc > m_i + kSlack;  // m_i = -inf: moves on the first visible score
     if (__any(move)) {
         const float m_new = move ? mloc : m_i;
         const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);  // 0 from -inf, 1 if not moved
@@ -159,7 +185,7 @@ __device__ __forceinline__ void online_exp(f32x16 &st, float mref, float &l_i) {
         st[r] = __builtin_amdgcn_exp2f(st[r] - mref);
         lsum += st[r];
     }
-    l_i += lsum + __shfl_xor(lsum, 32);
+    l_i += halves_sum(lsum);
 }
 
 template <int D>
@@ -226,7 +252,7 @@ __device__ __forceinline__ void merge_store(float *lds, const f32x16 (&o)[D / 32
 }
 
 // The general kernel: any head_dim <= D, any strides (K also pre-transposed), guarded loads.
-// A wave computes a 32-query group against key blocks w, w + ANW, ...:
+// A wave computes a 32-query group against key blocks first_block(w, qg), + ANW, ...:
 //   S^T = K Q'^T   A: K half rows, B: Q' half rows held for the whole kernel;
 //   online softmax in the lane (lane % 32 is the query) plus one exchange with lane ^ 32;
 //   O^T += V^T P^T A: V from the wave's LDS slab, B: the lane's own p registers.
@@ -319,7 +345,7 @@ void attn_fwd_kernel_f32(AttnArgs g) {
         block_pv<D>(o, st, vw, half, l31);
     };
 
-    int kb = wave;
+    int kb = first_block(wave, qg);
     if constexpr (D <= 64) {
         // two K stages, unrolled by two so neither is copied: block kb + ANW's K loads while kb
         // is multiplied
@@ -358,13 +384,16 @@ __device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 
 // The fast kernel: head_dim == D, Q / K / V / O rows contiguous and 16-byte aligned (K in
 // [N, D] order), every row offset of a head within 2^31 bytes (checked on the host). Per query
-// group it runs the general kernel's blocks and arithmetic (wave w takes key blocks w, w + ANW,
-// ..., the same online softmax and the same merge formula), so the two agree bit for bit:
+// group it runs the general kernel's blocks and arithmetic (wave w takes key blocks
+// first_block(w, qg), + ANW, ..., the same online softmax and the same merge formula), so the two
+// agree bit for bit:
 //   * Q, K and V come through buffer descriptors bounded at the head's last row. Loads past it
 //     return zeros, LDS-DMA loads included, so nothing is guarded and every block, the partial
 //     last one too, takes one code path (which also keeps the compiler's memory waits exact);
-//   * Q' (pre-scaled) lives in LDS transposed (qT[d][query]): the score product's B operand is
-//     a conflict-free LDS read instead of 32 registers per lane;
+//   * Q' (pre-scaled) is staged once per workgroup in LDS. The paired kernel (two waves per
+//     SIMD) loads a wave's B operand of the score product into 32 registers per group, so the
+//     product is MFMAs alone; the single-group kernel (three waves per SIMD, no registers to
+//     spare) keeps Q' transposed (qT[d][query]) and reads the operand per step, conflict-free;
 //   * V blocks are copied from memory straight into the wave's LDS slab (16-byte LDS-DMA);
 //   * software pipeline: block j+1's score product is issued beside block j's exps, K is loaded
 //     two blocks ahead and V one block ahead; Q is requested first and the first block's K
@@ -384,6 +413,29 @@ __device__ __forceinline__ f32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
+// The Q' tile of a query group in LDS: q2[j][d] = Q'[query j][d], the 16-byte chunks of row j
+// stored XOR-swizzled (chunk c at c ^ (j % (D/4))): the staging writes (a row's chunks from
+// consecutive lanes) and the operand reads (chunk c of 32 rows) fall on distinct banks.
+template <int D>
+__device__ __forceinline__ int q2_col(int j, int c) {
+    return (c ^ (j % (D / 4))) * 4;
+}
+
+// A lane's B operand of the score product, Q'[l31][half * D/2 + s] for s = 0 .. D/2-1 (the
+// contraction order of block_scores), read from the swizzled tile
+template <int D>
+__device__ __forceinline__ void load_q_operand(float (&qf)[D / 2], const float (*q2)[D], int half, int l31) {
+#pragma unroll
+    for (int c = 0; c < D / 8; c++) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(&q2[l31][q2_col<D>(l31, half * (D / 8) + c)]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) qf[4 * c + e] = v[e];
+    }
+}
+
+// block_scores with the B operand read from a transposed tile qT[d][query] (for kernels without
+// the registers to hold it): lane l31 of a step reads consecutive words, one immediate offset
+// per step from a single address
 template <int D>
 __device__ __forceinline__ f32x16 block_scores_lds(const float (&kf)[D / 2], const float (*qT)[AQG], int half,
                                                    int l31) {
@@ -461,6 +513,10 @@ void attn_fwd_fast(AttnArgs g) {
     __shared__ __attribute__((aligned(16))) float lds_q[QT_F > XM_F ? QT_F : XM_F];
     static_assert(!PAIR || sizeof(lds_v) + sizeof(lds_q) <= 80 * 1024, "two paired workgroups share a CU's 160 KB");
     float(*vslab)[ABN][D] = reinterpret_cast<float(*)[ABN][D]>(lds_v);
+    // the Q' tiles: row-major and swizzled (q2) when the operand is loaded into registers once
+    // per group, transposed (qT) when every score product reads it
+    constexpr bool QREG = PAIR || PITON_ATTN_FAST_WAVES <= 2;
+    float(*q2)[AQG][D] = reinterpret_cast<float(*)[AQG][D]>(lds_q);
     float(*qT)[D][AQG] = reinterpret_cast<float(*)[D][AQG]>(lds_q);
 
     const int t = threadIdx.x, lane = t & 63, half = lane >> 5, l31 = lane & 31;
@@ -483,14 +539,15 @@ void attn_fwd_fast(AttnArgs g) {
     const auto rk = make_rsrc(g.k + bi * g.s_kb + h * g.s_kh, ((uint32_t)(n_ctx - 1) * s_kn + D) * 4u);
     const auto rv = make_rsrc(g.v + bi * g.s_vb + h * g.s_vh, ((uint32_t)(n_ctx - 1) * s_vn + D) * 4u);
 
-    // this wave's blocks: list index j < n0 is block wave + ANW*j of the first group, j >= n0
-    // block wave + ANW*(j - n0) of the second (the heavier group comes first, so n0 >= n1)
+    // this wave's blocks: list index j < n0 is block f0 + ANW*j of the first group, j >= n0
+    // block f1 + ANW*(j - n0) of the second (the heavier group comes first)
     const int nkb_all = (n_ctx + ABN - 1) / ABN;
     const int nkb0 = g.causal ? min(nkb_all, qg0 + 1) : nkb_all, nkb1 = min(nkb_all, qg1 + 1);
-    const int n0 = nkb0 > wave ? (nkb0 - wave + ANW - 1) / ANW : 0;
-    const int n1 = (PAIR && ng > 1 && nkb1 > wave) ? (nkb1 - wave + ANW - 1) / ANW : 0;
+    const int f0 = first_block(wave, qg0), f1 = first_block(wave, qg1);
+    const int n0 = nkb0 > f0 ? (nkb0 - f0 + ANW - 1) / ANW : 0;
+    const int n1 = (PAIR && ng > 1 && nkb1 > f1) ? (nkb1 - f1 + ANW - 1) / ANW : 0;
     const int n = n0 + n1;
-    auto kb_of = [&](int j) { return wave + ANW * (j < n0 ? j : j - n0); };
+    auto kb_of = [&](int j) { return j < n0 ? f0 + ANW * j : f1 + ANW * (j - n0); };
 
     // byte offsets: K half row of key kb*32 + l31; V chunk c of block kb at v_lane + kb*v_blk + c*v_c
     constexpr int KPC = 64 / (D / 4);  // V keys per float4 chunk step of the lane
@@ -520,8 +577,8 @@ void attn_fwd_fast(AttnArgs g) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)&vw[KPC * c][0], 16, off + v_c * c, 0, 0, 0);
     };
 
-    // Q'^T of the groups: qT[gi][d][j] = Q[qg_gi*AQG + j][d] * sm_scale * log2 e (rows past
-    // n_ctx: 0). Every Q chunk is requested first, then the first block's K: the memory counter
+    // Q' of the groups: q2[gi][j][d] = qT[gi][d][j] = Q[qg_gi*AQG + j][d] * sm_scale * log2 e
+    // (rows past n_ctx: 0). Every Q chunk is requested first, then the first block's K: the memory counter
     // is in order, so the Q writes wait for Q alone while K is still in flight. Every wave
     // requests a first K block (one without blocks requests block `wave`, never used).
     constexpr int QIT = NG * AQG * D / 4 / (64 * ANW);
@@ -545,8 +602,15 @@ void attn_fwd_fast(AttnArgs g) {
     for (int c = 0; c < QIT; c++) {
         int gi, j, dq;
         q_chunk(c, gi, j, dq);
+        f32x4 w;
 #pragma unroll
-        for (int e = 0; e < 4; e++) qT[gi][4 * dq + e][j] = qv[c][e] * g.scale;
+        for (int e = 0; e < 4; e++) w[e] = qv[c][e] * g.scale;
+        if constexpr (QREG) {
+            *reinterpret_cast<f32x4 *>(&q2[gi][j][q2_col<D>(j, dq)]) = w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) qT[gi][4 * dq + e][j] = w[e];
+        }
     }
     // the other waves need the Q tiles only: wait for this wave's LDS writes and meet at the
     // barrier, without the release fence of __syncthreads, whose wait covers every memory
@@ -565,7 +629,12 @@ void attn_fwd_fast(AttnArgs g) {
     float m_i = -INFINITY, l_i = 0.f, pm = -INFINITY, pl = 0.f;
 
     if (n > 0) {
-        f32x16 st = block_scores_lds<D>(kf, qT[0], half, l31);
+        // the current group's Q' operand, in registers where the occupancy leaves room for it
+        float qf[D / 2];
+        // (a wave can hold no block of the first group and some of the second)
+        if constexpr (QREG) load_q_operand<D>(qf, q2[PAIR && n0 == 0 ? 1 : 0], half, l31);
+        auto scores = [&]() { return QREG ? block_scores<D>(kf, qf) : block_scores_lds<D>(kf, qT[0], half, l31); };
+        f32x16 st = scores();
         // Every pass of the loop starts with block j+1's K in flight ahead of block j's V, so
         // the wait for that K lets the newer V copies stay in flight. Block 0's V is therefore
         // requested after block 1's K: issued before it (as soon as Q is staged), the compiler
@@ -581,7 +650,10 @@ void attn_fwd_fast(AttnArgs g) {
             mask_scores(st, kb_of(j) * ABN, n_ctx, g.causal, q0, q0 + l31, half);
             const float mref = online_rescale<D>(st, m_i, l_i, o);
             f32x16 st_next;
-            if constexpr (NEXT) st_next = block_scores_lds<D>(kf, qT[PAIR && j + 1 >= n0 ? 1 : 0], half, l31);
+            if constexpr (NEXT) {
+                if (PAIR && j + 1 == n0) load_q_operand<D>(qf, q2[1], half, l31);  // j+1 opens group 2
+                st_next = scores();
+            }
             online_exp(st, mref, l_i);
             if constexpr (NEXT) load_k(kf, kb_of(j + 2));
             // block j's V is in the slab once at most the K loads just issued (D / 8 of them) are

@@ -235,7 +235,7 @@ __device__ __forceinline__ void merge_store(float *lds, const f32x16 (&o)[D / 32
 #pragma unroll
         for (int w = 0; w < ANW - 1; w++) {
             cw[w] = __builtin_amdgcn_exp2f(xm[w][0][lane] - mu);
-            l += xm[w][1][lane] * cw[w];
+            l = __builtin_fmaf(xm[w][1][lane], cw[w], l);
         }
         const float inv = 1.0f / l;
 #pragma unroll
@@ -245,7 +245,7 @@ __device__ __forceinline__ void merge_store(float *lds, const f32x16 (&o)[D / 32
                 const int d = b * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                 float acc = o[b][r] * c0;
 #pragma unroll
-                for (int w = 0; w < ANW - 1; w++) acc += xo[w][b * 16 + r][lane] * cw[w];
+                for (int w = 0; w < ANW - 1; w++) acc = __builtin_fmaf(xo[w][b * 16 + r][lane], cw[w], acc);
                 if (d < head_dim) op[d] = acc * inv;
             }
     }
@@ -463,8 +463,9 @@ __device__ __forceinline__ void map_pair(const AttnArgs &g, int64_t &bh, int &pr
 
 // One query group's merge from the ANW wave states in LDS (xo[w][slot][lane] with slot
 // b*16 + r for o[b][r], xm[w][0|1][lane] = m, l): merge_store's arithmetic (wave 0's state
-// first, then waves 1.. in order), wave w finishing slots [w*D/8, (w+1)*D/8) of every lane,
-// four consecutive dims per float4 store.
+// first, then waves 1.. in order, each added by a written-out fused multiply-add, so no kernel's
+// result depends on which product of a*b + c*d the compiler would fuse), wave w finishing slots
+// [w*D/8, (w+1)*D/8) of every lane, four consecutive dims per float4 store.
 template <int D>
 __device__ __forceinline__ void merge_quarter(const float (*xo)[D / 2][64], const float (*xm)[2][64], float *op,
                                               bool row_ok) {
@@ -479,7 +480,7 @@ __device__ __forceinline__ void merge_quarter(const float (*xo)[D / 2][64], cons
 #pragma unroll
     for (int w = 1; w < ANW; w++) {
         cw[w - 1] = __builtin_amdgcn_exp2f(xm[w][0][lane] - mu);
-        l += xm[w][1][lane] * cw[w - 1];
+        l = __builtin_fmaf(xm[w][1][lane], cw[w - 1], l);
     }
     const float inv = 1.0f / l;
     if (!row_ok) return;
@@ -492,7 +493,7 @@ __device__ __forceinline__ void merge_quarter(const float (*xo)[D / 2][64], cons
         for (int e = 0; e < 4; e++) {
             float acc = xo[0][s0 + e][lane] * c0;
 #pragma unroll
-            for (int w = 1; w < ANW; w++) acc += xo[w][s0 + e][lane] * cw[w - 1];
+            for (int w = 1; w < ANW; w++) acc = __builtin_fmaf(xo[w][s0 + e][lane], cw[w - 1], acc);
             v[e] = acc * inv;
         }
         *reinterpret_cast<f32x4 *>(op + b * 32 + 8 * (r >> 2) + 4 * half) = v;

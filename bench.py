@@ -281,6 +281,25 @@ def bench_softmax(n, rows=4096, launches=48, sample_rows=256):
     return line, sample
 
 
+def bench_mfma_sustained(cus, iters=2000):
+    """The device's sustained fp32 MFMA rate in this run (piton_mi355x_mfma_probe: two waves
+    per SIMD, two independent 32x32x2 chains each), and the engine clock it implies (one
+    4096-flop MFMA per 64 clocks per SIMD). The published peak assumes 2.4 GHz; each MFMA
+    fraction is also given against the rate measured here, so a fraction below 1 is the
+    kernel's and not the clock's."""
+    import torch
+
+    from piton_amd.runtime import mi355x as rt
+    wgs = 2 * cus
+    out = torch.empty(wgs * 256, device="cuda")
+    avg = timed_graph(lambda i: rt.mfma_probe(out, wgs, iters), 4)
+    flops = wgs * 4 * iters * 32 * 4096
+    rate = flops / avg
+    return dict(tflops=round(rate / 1e12, 2), clock_ghz=round(rate / (cus * 4 * 64) / 1e9, 3),
+                frac_of_published=round(rate / PEAK_FP32_MFMA, 4), launch_ms=round(avg * 1e3, 3),
+                probe="piton_mi355x_mfma_probe, %d workgroups x 4 waves x %d x 32 MFMAs" % (wgs, iters))
+
+
 def bench_attention(launches=32):
     import torch
 
@@ -574,6 +593,9 @@ def main():
                      "kernel_us": round(avg * 1e6, 2), "kernel": mm["kernel"], "traffic_source": traffic_source()},
         "device": {k: info[k] for k in ("arch", "cu_count", "max_clock_khz", "hbm_bytes")},
     }
+    sustained = bench_mfma_sustained(info["cu_count"])
+    line["mfma_sustained"] = sustained
+    line["roofline"]["frac_of_sustained"] = round(achieved / (sustained["tflops"] * 1e12), 4)
     a_host, b_host = (mm["a"].cpu(), mm["b"].cpu()) if not args.no_cpu else (None, None)
     c_rows = mm["c"][:64].cpu().numpy() if not args.no_cpu else None
     del mm
@@ -587,6 +609,7 @@ def main():
             sm, samples[f"softmax {nc}"] = bench_softmax(nc)
             line["softmax"].append(sm)
         line["attention"], samples["attention"] = bench_attention()
+        line["attention"]["frac_of_sustained"] = round(line["attention"]["tflops"] / sustained["tflops"], 4)
         line["mlp"], samples["mlp"] = bench_mlp()
         line["tinygpt"], samples["tinygpt"] = bench_tinygpt()
     if not args.no_cpu:  # last: the GPU idles while the host cores work

@@ -232,6 +232,15 @@ PITON_API int32_t piton_mi355x_row_max(const float *x, float *out, int64_t rows,
 PITON_API int32_t piton_mi355x_transpose(const float *x, float *out, int64_t n_rows, int64_t n_cols,
                                          int64_t stride_x, int64_t stride_out, void *stream);
 
+/* ---- diagnostics ---- */
+
+/* The sustained fp32 MFMA rate, measured: `workgroups` workgroups of four waves each issue
+ * iters x 32 v_mfma_f32_32x32x2_f32 (4096 flops each) in two independent chains; the caller
+ * times the launch on `stream`. out holds workgroups x 256 floats (written, meaningless). No
+ * counterpart in the reference: it measures the MFMA roofline of the device at hand beside the
+ * published peak, which assumes the 2.4 GHz peak engine clock. */
+PITON_API int32_t piton_mi355x_mfma_probe(float *out, int64_t workgroups, int32_t iters, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

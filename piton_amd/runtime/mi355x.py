@@ -63,6 +63,7 @@ SIGNATURES = {
     "piton_mi355x_attn_fwd_batched": [_p, _p, _p, _p, _f32] + [_i64] * 16 + [_i32, _i32, _p],
     "piton_mi355x_attn_decode": [_p, _p, _p, _p, _f32] + [_i64] * 13 + [_i32, _p],
     "piton_mi355x_copy": [_p, _p, _i64, _p],
+    "piton_mi355x_mfma_probe": [_p, _i64, _i32, _p],
     "piton_mi355x_mul": [_p, _p, _p, _i64, _p],
     "piton_mi355x_fma": [_p, _p, _p, _i64, _f32, _p],
     "piton_mi355x_scaled_relu": [_p, _p, _i64, _f32, _p],
@@ -344,6 +345,14 @@ def _elementwise(entry, n, tensors, *scalars):
     for name, t in tensors:
         check_tensor(name, t, max_offset=n - 1)
     _call(entry, *[_ptr(t) for _, t in tensors], n, *scalars, _stream())
+
+
+def mfma_probe(out, workgroups, iters):
+    """Diagnostics (no reference counterpart): workgroups x 4 waves each issue iters x 32 fp32
+    32x32x2 MFMAs in two independent chains; the caller times the launch. out: float32, at
+    least workgroups * 256 elements."""
+    check_tensor("out", out, max_offset=int(workgroups) * 256 - 1)
+    _call("piton_mi355x_mfma_probe", _ptr(out), int(workgroups), int(iters), _stream())
 
 
 def copy(x, out, n):

@@ -48,16 +48,19 @@ def _newer(src: str, obj: str, deps) -> bool:
     return any(os.path.getmtime(p) > t for p in [src, *deps])
 
 
-def build(verbose: bool = False, incremental: bool = False, extra_flags=()) -> str:
-    os.makedirs(OBJ, exist_ok=True)
-    os.makedirs(LIB_DIR, exist_ok=True)
+def build(verbose: bool = False, incremental: bool = False, extra_flags=(), obj_dir: str = OBJ,
+          lib: str = LIB) -> str:
+    """Compiles every csrc/*.hip for gfx950 into obj_dir and links `lib` (by default the product
+    library; piton_amd.phase_trace builds its traced copy beside it with its own paths)."""
+    os.makedirs(obj_dir, exist_ok=True)
+    os.makedirs(os.path.dirname(lib), exist_ok=True)
     cc = hipcc()
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     deps = glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(ROOT, "include", "*.h"))
     flags = COMMON_FLAGS + list(extra_flags)
 
     def compile_one(src):
-        obj = os.path.join(OBJ, os.path.basename(src)[:-4] + ".o")
+        obj = os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o")
         if incremental and not _newer(src, obj, deps):
             return obj, ""
         cmd = [cc, *flags, "-c", src, "-o", obj + ".tmp"]
@@ -74,14 +77,14 @@ def build(verbose: bool = False, incremental: bool = False, extra_flags=()) -> s
             if err.strip():
                 print(f"--- {os.path.basename(obj)}\n{err}")
     objs = [o for o, _ in results]
-    tmp = LIB + ".tmp"
+    tmp = lib + ".tmp"
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
            "-Wl,-rpath,/opt/rocm/lib", "-Wl,--no-undefined"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":

@@ -57,6 +57,7 @@ struct AttnArgs {
     int q_vec;  // Q rows loadable as float4
     int v_vec;  // V rows loadable as float4
     int nqg, nbh;  // query groups per head, batch * heads (the 1-D grid is nqg * nbh)
+    PhaseRecord *phase;  // the launch's phase-trace records (diagnostics builds; null otherwise)
 };
 
 // MFMA k-index of the score product: lane half h carries head dims [h*D/2, (h+1)*D/2), step s
@@ -522,6 +523,8 @@ void attn_fwd_fast(AttnArgs g) {
 
     const int t = threadIdx.x, lane = t & 63, half = lane >> 5, l31 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    PITON_PHASE_VARS;
+    PITON_PHASE(0);
     int64_t bh;
     int qg0, qg1 = 0, ng = 1;
     if constexpr (PAIR) {
@@ -621,6 +624,7 @@ void attn_fwd_fast(AttnArgs g) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     __builtin_amdgcn_sched_barrier(0);
+    PITON_PHASE(1);
 
     f32x16 o[D / 32], po[D / 32];  // the running state and (PAIR) the parked first group's
 #pragma unroll
@@ -704,6 +708,7 @@ void attn_fwd_fast(AttnArgs g) {
         xm[wave][0][lane] = sm;
         xm[wave][1][lane] = sl;
     };
+    PITON_PHASE(2);
     // every V copy into the slabs has landed before the LDS is reused for the merge
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();  // every wave is done with its slab and the Q tiles
@@ -716,6 +721,8 @@ void attn_fwd_fast(AttnArgs g) {
         merge_quarter<D>(xo_of(gi), xm_of(gi),
                          g.o + bi * g.s_ob + h * g.s_oh + (int64_t)qi * g.s_om, qi < n_ctx);
     }
+    PITON_PHASE(3);
+    PITON_PHASE_END(kPhaseAttnFast, g.phase);
 }
 
 template <int D>
@@ -931,6 +938,7 @@ static int attn_launch(AttnArgs g, int64_t batch, int64_t n_heads, int32_t head_
                     head_dim % 4 == 0) ? K_VEC_D : K_SCALAR;
     g.nqg = (int)((g.n_ctx + AQG - 1) / AQG);
     g.nbh = (int)(batch * n_heads);
+    g.phase = phase_slot();
     dim3 grid((unsigned)((int64_t)g.nqg * g.nbh));
     // the fast kernel: exact head_dim, contiguous aligned rows that do not overlap, and every
     // byte offset it forms (rows up to n_ctx + 3 * ANW * 32, the loads a few blocks past the
@@ -975,6 +983,8 @@ static int attn_check(const float *q, const float *k, const float *v, const floa
 }
 
 }  // namespace piton
+
+PITON_PHASE_TU(attention)
 
 extern "C" {
 

@@ -37,6 +37,64 @@ void reset_launches();
         hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                                   \
     } while (0)
 
+// ------------------------------------------------------------------------------------------
+// Phase trace (diagnostics builds only, -DPITON_PHASE_TRACE; piton_amd/phase_trace.py): a traced
+// wave keeps up to four s_memrealtime stamps (a 100 MHz clock shared by the whole chip) in
+// registers and, at its end, lane 0 stores them into the wave's own record of the launch's
+// record area (no atomics, so waves do not wait on each other). The host hands each launch its
+// own area (phase_slot(), a kernel argument that is null in the product build, where every
+// macro below is empty); PITON_PHASE_TU(name) exports piton_phase_attach_<name>(log, launches)
+// for the source file's launches, which cycle through `launches` areas of kPhaseWaves records.
+// ------------------------------------------------------------------------------------------
+struct PhaseRecord {
+    unsigned long long t[4];
+    uint32_t kernel, block;
+};
+constexpr uint32_t kPhaseWaves = 1u << 16;  // records per launch: waves past it are not traced
+#ifdef PITON_PHASE_TRACE
+static PhaseRecord *g_phase_base = nullptr;
+static unsigned int g_phase_launches = 0, g_phase_seq = 0;
+static inline PhaseRecord *phase_slot() {
+    return g_phase_base ? g_phase_base + (size_t)(g_phase_seq++ % g_phase_launches) * kPhaseWaves : nullptr;
+}
+#define PITON_PHASE_VARS unsigned long long _phase_t[4] = {0ull, 0ull, 0ull, 0ull}
+#define PITON_PHASE(i)                                        \
+    do {                                                      \
+        __builtin_amdgcn_sched_barrier(0);                    \
+        _phase_t[i] = __builtin_amdgcn_s_memrealtime();       \
+        __builtin_amdgcn_sched_barrier(0);                    \
+    } while (0)
+// the wave's loads in flight have landed (the stamp after it marks the first data)
+#define PITON_PHASE_WAIT_LOADS() __builtin_amdgcn_s_waitcnt(0x0F70)
+#define PITON_PHASE_END(kid, area)                                                                   \
+    do {                                                                                             \
+        const uint32_t _w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);                     \
+        if ((area) && (threadIdx.x & 63) == 0 && _w < ::piton::kPhaseWaves) {                        \
+            ::piton::PhaseRecord *_r = (area) + _w;                                                  \
+            for (int _k = 0; _k < 4; _k++) _r->t[_k] = _phase_t[_k];                                 \
+            _r->kernel = (kid);                                                                      \
+            _r->block = _w;                                                                          \
+        }                                                                                            \
+    } while (0)
+#define PITON_PHASE_TU(name)                                                                             \
+    extern "C" __attribute__((visibility("default"))) int piton_phase_attach_##name(void *log,           \
+                                                                                     unsigned int launches) { \
+        ::piton::g_phase_base = launches ? (::piton::PhaseRecord *)log : nullptr;                        \
+        ::piton::g_phase_launches = launches;                                                            \
+        ::piton::g_phase_seq = 0;                                                                        \
+        return 0;                                                                                        \
+    }
+#else
+static inline PhaseRecord *phase_slot() { return nullptr; }
+#define PITON_PHASE_VARS
+#define PITON_PHASE(i)
+#define PITON_PHASE_WAIT_LOADS()
+#define PITON_PHASE_END(kid, area)
+#define PITON_PHASE_TU(name)
+#endif
+// kernel ids of the trace records
+constexpr uint32_t kPhaseSoftmaxRows = 1, kPhaseSoftmaxWg = 2, kPhaseAttnFast = 3;
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 

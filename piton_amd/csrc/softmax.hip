@@ -171,7 +171,7 @@ __device__ __forceinline__ void softmax_store_row(float *out, int64_t out_rs, in
 // rows themselves and only whole chunks need a bound. Rows here are <= 2048 columns.
 template <int CH, bool ALIGNED>
 __global__ __launch_bounds__(256) void softmax_rows_kernel(float *out, const float *in, int64_t in_rs, int64_t out_rs,
-                                                           int n, int64_t rows) {
+                                                           int n, int64_t rows, PhaseRecord *phase) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t W = (int64_t)gridDim.x * 4;
     int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -179,7 +179,11 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float *out, const flo
 
     f32x4 a[CH], b[CH];
     int off_a, off_b = 0;
+    PITON_PHASE_VARS;
+    PITON_PHASE(0);
     load_row<CH, 64, ALIGNED>(in, in_rs, row, n, lane, a, off_a);
+    PITON_PHASE_WAIT_LOADS();
+    PITON_PHASE(1);
     while (true) {
         if (row + W < rows) load_row<CH, 64, ALIGNED>(in, in_rs, row + W, n, lane, b, off_b);
         softmax_store_row<CH, 64, ALIGNED>(out, out_rs, row, n, lane, a, off_a, nullptr);
@@ -190,6 +194,8 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float *out, const flo
         row += W;
         if (row >= rows) break;
     }
+    PITON_PHASE(2);
+    PITON_PHASE_END(kPhaseSoftmaxRows, phase);
 }
 
 // One T-thread workgroup per row (T = 256 or 512, CH chunks per thread): many short-lived
@@ -197,12 +203,18 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float *out, const flo
 // generation of row-per-wave waves.
 template <int CH, int T, bool ALIGNED>
 __global__ __launch_bounds__(T) void softmax_wg_kernel(float *out, const float *in, int64_t in_rs, int64_t out_rs,
-                                                       int n) {
+                                                       int n, PhaseRecord *phase) {
     __shared__ float red[2 * T / 64];
     f32x4 b[CH];
     int off;
+    PITON_PHASE_VARS;
+    PITON_PHASE(0);
     load_row<CH, T, ALIGNED>(in, in_rs, blockIdx.x, n, threadIdx.x, b, off);
+    PITON_PHASE_WAIT_LOADS();
+    PITON_PHASE(1);
     softmax_store_row<CH, T, ALIGNED>(out, out_rs, blockIdx.x, n, threadIdx.x, b, off, red);
+    PITON_PHASE(2);
+    PITON_PHASE_END(kPhaseSoftmaxWg, phase);
 }
 
 // Rows too long for registers: one workgroup per row, three passes over the row.
@@ -256,10 +268,12 @@ void launch_rows(int mode, int64_t wgs, hipStream_t st, float *out, const float 
         grid = wgs < cap ? wgs : cap;
     }
     PITON_LAUNCH((softmax_rows_kernel<CH, ALIGNED>), dim3((unsigned)grid), dim3(256), 0, st, out, in, in_rs,
-                       out_rs, n, rows);
+                       out_rs, n, rows, phase_slot());
 }
 
 }  // namespace piton
+
+PITON_PHASE_TU(softmax)
 
 extern "C" int32_t piton_mi355x_softmax(float *out, const float *in, int64_t in_row_stride, int64_t out_row_stride,
                                         int64_t n_cols, int64_t n_rows, int64_t block_size, void *stream) {
@@ -297,10 +311,10 @@ extern "C" int32_t piton_mi355x_softmax(float *out, const float *in, int64_t in_
     do {                                                                                                            \
         if (aligned)                                                                                                \
             PITON_LAUNCH((softmax_wg_kernel<CH, T, true>), dim3((unsigned)n_rows), dim3(T), 0, st, out, in,   \
-                               in_row_stride, out_row_stride, (int)n);                                              \
+                               in_row_stride, out_row_stride, (int)n, phase_slot());                                \
         else                                                                                                        \
             PITON_LAUNCH((softmax_wg_kernel<CH, T, false>), dim3((unsigned)n_rows), dim3(T), 0, st, out, in,  \
-                               in_row_stride, out_row_stride, (int)n);                                              \
+                               in_row_stride, out_row_stride, (int)n, phase_slot());                                \
     } while (0)
     PITON_REQUIRE(mode != 2 || n_rows <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "softmax: too many rows");
     PITON_REQUIRE(mode == 2 || wgs <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "softmax: too many rows");

@@ -1,0 +1,146 @@
+"""Launch phases of the HBM-bound softmax and the one-generation attention kernel (diagnostics).
+
+`python -m piton_amd.phase_trace` builds a traced copy of the library beside the product one
+(-DPITON_PHASE_TRACE: every traced wave keeps s_memrealtime stamps -- a 100 MHz clock shared by
+the whole chip -- and stores one record into its own slot at its end; the product build
+compiles none of it), replays launches back to back from a HIP graph as bench.py does (each
+launch writes its own record area, handed to it by the host) and prints, per workload, the
+median over the launches of: when the last wave started, when the first wave had its first row
+(softmax) or its Q tile (attention), each wave's own wait for it, when the last wave finished,
+and the gap to the next launch's first wave. For softmax the bytes over the window from first
+data to last wave end give the streaming rate while the kernel runs, apart from its start and
+its drain.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import os
+import statistics
+
+from . import build as _build
+
+TRACE_LIB = os.path.join(_build.LIB_DIR, "libpiton_mi355x_trace.so")
+TRACE_OBJ = os.path.join(_build.HERE, "_build_trace")
+TICK_US = 0.01  # s_memrealtime: 100 MHz
+K_PHASE_WAVES = 1 << 16  # records per launch area (kPhaseWaves in csrc/common.h)
+
+
+class Record(ctypes.Structure):
+    _fields_ = [("t", ctypes.c_uint64 * 4), ("kernel", ctypes.c_uint32), ("block", ctypes.c_uint32)]
+
+
+def build_traced(verbose: bool = False) -> str:
+    return _build.build(verbose=verbose, extra_flags=["-DPITON_PHASE_TRACE"], obj_dir=TRACE_OBJ, lib=TRACE_LIB)
+
+
+def _trace(tu: str, fn, launches: int):
+    """Stamps of `launches` back-to-back launches replayed from a HIP graph, one list per launch
+    (the i-th launch after the attach writes area i)."""
+    import numpy as np
+    import torch
+
+    from .runtime import mi355x as rt
+    L = rt.lib()
+    attach = getattr(L, f"piton_phase_attach_{tu}")
+    attach.argtypes, attach.restype = [ctypes.c_void_p, ctypes.c_uint], ctypes.c_int
+    rec = ctypes.sizeof(Record)
+    log = torch.zeros(launches * K_PHASE_WAVES * rec, dtype=torch.uint8, device="cuda")
+    assert attach(None, 0) == 0
+    fn(0)
+    torch.cuda.synchronize()
+    graph_off = torch.cuda.CUDAGraph()  # records off: brings the clocks up
+    with torch.cuda.graph(graph_off):
+        for i in range(launches):
+            fn(i)
+    assert attach(ctypes.c_void_p(log.data_ptr()), launches) == 0
+    graph = torch.cuda.CUDAGraph()  # the same launches, each with its own record area
+    with torch.cuda.graph(graph):
+        for i in range(launches):
+            fn(i)
+    assert attach(None, 0) == 0
+    for _ in range(20):
+        graph_off.replay()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    t = np.frombuffer(log.cpu().numpy().tobytes(), dtype=np.uint64).reshape(launches, K_PHASE_WAVES, rec // 8)
+    return [[tuple(int(x) for x in r[:4]) for r in t[k][t[k][:, 0] > 0]] for k in range(launches)]
+
+
+def _summary(launches, stamps: int, nbytes: int | None = None):
+    """Medians over the launches (the first and the last left out) of the phases, in us from the
+    launch's first wave start."""
+    rows = []
+    last = stamps - 1
+    for k in range(1, len(launches) - 1):
+        ls, nxt = launches[k], launches[k + 1]
+        t0 = min(r[0] for r in ls)
+        d = dict(waves=len(ls), last_wave_start=max(r[0] for r in ls) - t0,
+                 first_data=min(r[1] for r in ls) - t0,
+                 wave_wait=statistics.median(r[1] - r[0] for r in ls),
+                 end=max(r[last] for r in ls) - t0,
+                 gap_to_next=min(r[0] for r in nxt) - max(r[last] for r in ls))
+        if stamps == 4:
+            d["loop"] = statistics.median(r[2] - r[1] for r in ls)
+            d["merge"] = statistics.median(r[3] - r[2] for r in ls)
+        rows.append(d)
+    med = {k: statistics.median(r[k] for r in rows) * (1 if k == "waves" else TICK_US) for k in rows[0]}
+    if nbytes:
+        med["stream_tbs"] = nbytes / ((med["end"] - med["first_data"]) * 1e-6) / 1e12
+    return med
+
+
+def softmax_phases(n: int, rows: int = 4096, launches: int = 12):
+    import torch
+
+    from . import next_power_of_2
+    from .runtime import mi355x as rt
+    pair_bytes = 2 * 4 * rows * n
+    pairs = max(2, -(-2 ** 30 // (pair_bytes // 2)))  # inputs over >= 1 GiB: every launch reads HBM
+    g = torch.Generator(device="cuda").manual_seed(n)
+    xs = [torch.randn((rows, n), device="cuda", generator=g) * 4 for _ in range(pairs)]
+    ys = [torch.empty_like(x) for x in xs]
+    block = next_power_of_2(n)
+    per = _trace("softmax", lambda i: rt.softmax(ys[i % pairs], xs[i % pairs], n, n, n, rows, block), launches)
+    return _summary([[r[:3] for r in ls] for ls in per], 3, pair_bytes)
+
+
+def attention_phases(heads: int = 32, n: int = 1024, d: int = 64, launches: int = 12):
+    import torch
+
+    from .runtime import mi355x as rt
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q, k, v = (torch.randn((heads, n, d), device="cuda", generator=g) for _ in range(3))
+    o = torch.empty_like(q)
+    per = _trace("attention", lambda i: rt.attn_fwd(q, k, v, o, d ** -0.5, n * d, d, n * d, d, 1, n * d, d, n * d, d,
+                                                    n, heads, d, True), launches)
+    return _summary(per, 4)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--no-build", action="store_true", help="use the traced library already built")
+    a = ap.parse_args()
+    if not a.no_build:
+        build_traced()
+    os.environ["PITON_MI355X_LIB"] = TRACE_LIB  # before the runtime loads a library
+
+    def us(v):
+        return f"{v:.2f} us"
+
+    print("| workload | waves | last wave starts | first data | a wave's own wait | last wave ends | "
+          "gap to next launch | streaming between first data and end |")
+    print("|---|---|---|---|---|---|---|---|")
+    for n in (1024, 4096, 1823):
+        m = softmax_phases(n)
+        print(f"| softmax 4096 x {n} | {int(m['waves'])} | {us(m['last_wave_start'])} | {us(m['first_data'])} | "
+              f"{us(m['wave_wait'])} | {us(m['end'])} | {us(m['gap_to_next'])} | {m['stream_tbs']:.2f} TB/s |")
+    m = attention_phases()
+    print(f"| attention 32 x 1024 x 64 causal | {int(m['waves'])} | {us(m['last_wave_start'])} | "
+          f"{us(m['first_data'])} (Q staged) | {us(m['wave_wait'])} | {us(m['end'])} | {us(m['gap_to_next'])} | "
+          f"per wave: loop {us(m['loop'])}, merge {us(m['merge'])} |")
+
+
+if __name__ == "__main__":
+    main()

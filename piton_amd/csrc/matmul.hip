@@ -746,26 +746,55 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
     const int64_t m = m0 + c16;  // the A row this lane supplies
     const bool m_ok = m < g.M;
     f32x4v acc = f32x4v{0.f, 0.f, 0.f, 0.f};
+    // the epilogue's bias and residual, requested now: thread (r, lane) = (t / 64, t % 64) < 256
+    // finishes output (m0 + 4*grp + r, n), and only it reads and writes that element (so a
+    // residual that is the output itself is read before it is written)
+    const int er = t >> 6;
+    const int64_t emo = m0 + 4 * grp + er;
+    const bool e_ok = t < 256 && emo < g.M && n_ok;
+    const float e_bias = (e_ok && g.bias) ? g.bias[n] : 0.f;
+    const float e_res = (e_ok && g.res) ? g.res[emo * g.s_rm + n] : 0.f;
     float ln_mean = 0.f, ln_inv = 1.f;
-    if constexpr (LN) {
-        // wave w: the statistics of row m0 + w (K % 256 == 0, so a lane's chunks are lane + 64c)
+    // LN: wave w computes the statistics of row m0 + w (K % 256 == 0, so a lane's chunks are
+    // lane + 64c); a row of up to 1024 columns stays in registers for the variance pass
+    auto ln_stats = [&]() {
+        constexpr int MAXC = 4;
         const int64_t mr = m0 + wave;
         if (mr < g.M) {
             const f32x4v *src = reinterpret_cast<const f32x4v *>(g.a + mr * g.s_am);
             const int64_t nch = g.K / 4;
-            float sum = 0.f;
-            for (int64_t ci = lane; ci < nch; ci += 64) {
-                const f32x4v f = src[ci];
-                sum += (f[0] + f[1]) + (f[2] + f[3]);
-            }
-            const float mean = wave_reduce(sum, SumOp()) / (float)g.K;
-            float q = 0.f;
-            for (int64_t ci = lane; ci < nch; ci += 64) {
-                const f32x4v f = src[ci];
+            float sum = 0.f, q = 0.f, mean;
+            if (nch <= 64 * MAXC) {
+                f32x4v ch[MAXC];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float d = f[j] - mean;
-                    q = fmaf(d, d, q);
+                for (int c = 0; c < MAXC; c++)
+                    if (lane + 64 * c < nch) ch[c] = src[lane + 64 * c];
+#pragma unroll
+                for (int c = 0; c < MAXC; c++)
+                    if (lane + 64 * c < nch) sum += (ch[c][0] + ch[c][1]) + (ch[c][2] + ch[c][3]);
+                mean = wave_reduce(sum, SumOp()) / (float)g.K;
+#pragma unroll
+                for (int c = 0; c < MAXC; c++)
+                    if (lane + 64 * c < nch) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const float d = ch[c][j] - mean;
+                            q = fmaf(d, d, q);
+                        }
+                    }
+            } else {
+                for (int64_t ci = lane; ci < nch; ci += 64) {
+                    const f32x4v f = src[ci];
+                    sum += (f[0] + f[1]) + (f[2] + f[3]);
+                }
+                mean = wave_reduce(sum, SumOp()) / (float)g.K;
+                for (int64_t ci = lane; ci < nch; ci += 64) {
+                    const f32x4v f = src[ci];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float d = f[j] - mean;
+                        q = fmaf(d, d, q);
+                    }
                 }
             }
             const float var = wave_reduce(q, SumOp()) / (float)g.K;
@@ -779,23 +808,26 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
             ln_mean = stats[c16][0];
             ln_inv = stats[c16][1];
         }
-    }
+    };
     if constexpr (FAST) {
         // kq % 4 == 0 and every k of the range < K; rows past M and columns past N read zeros
         const float *wp = g.b + (n_ok ? n : 0) + kbeg * g.s_bk;
         const float *xp = g.a + (m_ok ? m : 0) * g.s_am + kbeg;
+        // the raw loads; the normalisation (LN) and the row mask are applied by `ready`
         auto load = [&](int64_t s, f32x4v &xa, float (&wb)[4]) {
-            f32x4v v = *reinterpret_cast<const f32x4v *>(xp + s);
-            if constexpr (LN) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) v[j] = (v[j] - ln_mean) * ln_inv;
-            }
-            xa = m_ok ? v : f32x4v{0.f, 0.f, 0.f, 0.f};
+            xa = *reinterpret_cast<const f32x4v *>(xp + s);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const float w = wp[(s + j) * g.s_bk];
                 wb[j] = n_ok ? w : 0.f;
             }
+        };
+        auto ready = [&](f32x4v &xa) {
+            if constexpr (LN) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) xa[j] = (xa[j] - ln_mean) * ln_inv;
+            }
+            xa = m_ok ? xa : f32x4v{0.f, 0.f, 0.f, 0.f};
         };
         auto mul = [&](const f32x4v &xa, const float (&wb)[4]) {
 #pragma unroll
@@ -803,12 +835,15 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
         };
         f32x4v xa0, xa1;
         float wb0[4], wb1[4];
-        load(0, xa0, wb0);
+        load(0, xa0, wb0);  // in flight while the LN statistics are computed
+        if constexpr (LN) ln_stats();
         for (int64_t s = 0; s < kq; s += 8) {
             if (s + 4 < kq) load(s + 4, xa1, wb1);
+            ready(xa0);
             mul(xa0, wb0);
             if (s + 4 >= kq) break;
             if (s + 8 < kq) load(s + 8, xa0, wb0);
+            ready(xa1);
             mul(xa1, wb1);
         }
     } else {
@@ -833,9 +868,9 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
     float v = part[0][r][lane];
 #pragma unroll
     for (int w = 1; w < SMWAVES; w++) v += part[w][r][lane];
-    if (g.bias) v += g.bias[n];
+    if (g.bias) v += e_bias;
     if (g.relu && v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
-    if (g.res) v += g.res[mo * g.s_rm + n];
+    if (g.res) v += e_res;
     g.c[mo * g.s_cm + n] = v;
 }
 

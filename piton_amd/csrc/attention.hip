@@ -128,7 +128,7 @@ __device__ __forceinline__ f32x16 block_scores(const float (&kf)[D / 2], const f
 // The two halves of a wave hold the two halves of a query's keys. v_permlane32_swap of a value
 // with itself leaves the low half's values in every lane of one result and the high half's in
 // every lane of the other: a VALU exchange, no LDS round trip. max and + are commutative, so
-// every lane gets the value of the lane-order expression max(x, x^32) / x + x^32.
+// every lane gets the value fmaxf(x, __shfl_xor(x, 32)) or x + __shfl_xor(x, 32) would give it.
 __device__ __forceinline__ float halves_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));

@@ -178,14 +178,21 @@ void mlp3_fixed_kernel(const float *x, int64_t M, const float *w1, const float *
     __syncthreads();
     mlp_layer_regs<N2, N3, P3>(buf[0], wr3, b3, false, buf[1]);
     __syncthreads();
+#pragma unroll
     for (int idx = t; idx < MLP_ROWS * N3; idx += 256) {
         const int row = idx / N3, c = idx % N3;
         if (r0 + row < M && logits) logits[(r0 + row) * N3 + c] = buf[1][row][c];
     }
     if (t < MLP_ROWS && r0 + t < M && pred) {
+        // every logit of the row read first (one LDS round trip), then combined in class order
+        float lv[N3];
+#pragma unroll
+        for (int c = 0; c < N3; c++) lv[c] = buf[1][t][c];
         float bv = -INFINITY;
         int bi = 0x7FFFFFFF;
-        for (int c = 0; c < n_classes; c++) mlp_argmax_combine(bv, bi, buf[1][t][c], c);
+#pragma unroll
+        for (int c = 0; c < N3; c++)
+            if (c < n_classes) mlp_argmax_combine(bv, bi, lv[c], c);
         pred[r0 + t] = bi;
     }
 }

@@ -747,6 +747,7 @@ struct DecodeArgs {
     float scale;  // sm_scale * log2(e)
     int64_t s_qb, s_qh, s_kb, s_kh, s_kn, s_vb, s_vh, s_vn, s_ob, s_oh;
     int n_keys, n_heads, head_dim;
+    PhaseRecord *phase;  // the launch's phase-trace records (diagnostics builds; null otherwise)
 };
 
 template <class Op>
@@ -853,6 +854,8 @@ __global__ __launch_bounds__(256) void attn_decode_short(DecodeArgs g) {
     const bool dims_ok = d0 < head_dim;
     const int d = t % D, kg = t / D;
     const bool d_ok = d < head_dim;
+    PITON_PHASE_VARS;
+    PITON_PHASE(0);
 
     f32x4 kv[NIT][4];
 #pragma unroll
@@ -883,6 +886,8 @@ __global__ __launch_bounds__(256) void attn_decode_short(DecodeArgs g) {
 #pragma unroll
     for (int i = 0; i < 16; i++) q16[i] = dims_ok ? qp[d0 + i] * g.scale : 0.f;
 
+    PITON_PHASE_WAIT_LOADS();
+    PITON_PHASE(1);
     float mloc = -INFINITY;
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
@@ -906,6 +911,7 @@ __global__ __launch_bounds__(256) void attn_decode_short(DecodeArgs g) {
     }
     for (int j = n_keys + t; j < kShortDecodeKeys; j += 256) p[j] = 0.f;  // weights of absent keys
     const float m = block_reduce4(mloc, MaxOp(), red);
+    PITON_PHASE(2);
     float lsum = 0.f;
     for (int j = t; j < n_keys; j += 256) {
         const float e = __builtin_amdgcn_exp2f(p[j] - m);
@@ -929,6 +935,8 @@ __global__ __launch_bounds__(256) void attn_decode_short(DecodeArgs g) {
         for (int w = 1; w < KG; w++) v += part[w * D + t];
         g.o[b * g.s_ob + h * g.s_oh + t] = v * inv;
     }
+    PITON_PHASE(3);
+    PITON_PHASE_END(kPhaseAttnDecodeShort, g.phase);
 }
 
 static int attn_launch(AttnArgs g, int64_t batch, int64_t n_heads, int32_t head_dim, hipStream_t st) {
@@ -1044,7 +1052,8 @@ int32_t piton_mi355x_attn_decode(const float *q, const float *k, const float *v,
     if (rc) return rc;
     if (batch * n_heads == 0) return PITON_OK;
     DecodeArgs g{q, k, v, out, sm_scale * 1.44269504088896341f, stride_qb, stride_qh, stride_kb, stride_kh, stride_kn,
-                 stride_vb, stride_vh, stride_vn, stride_ob, stride_oh, (int)n_keys, (int)n_heads, head_dim};
+                 stride_vb, stride_vh, stride_vn, stride_ob, stride_oh, (int)n_keys, (int)n_heads, head_dim,
+                 phase_slot()};
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)(batch * n_heads)), block(256);
     const bool vec = aligned16(k) && stride_kn % 4 == 0 && stride_kh % 4 == 0 && stride_kb % 4 == 0;

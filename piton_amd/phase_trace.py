@@ -1,4 +1,5 @@
-"""Launch phases of the HBM-bound softmax and the one-generation attention kernel (diagnostics).
+"""Launch phases of the HBM-bound softmax, the one-generation attention kernel and the decode
+attention of the KV-cached decoder (diagnostics).
 
 `python -m piton_amd.phase_trace` builds a traced copy of the library beside the product one
 (-DPITON_PHASE_TRACE: every traced wave keeps s_memrealtime stamps -- a 100 MHz clock shared by
@@ -118,6 +119,24 @@ def attention_phases(heads: int = 32, n: int = 1024, d: int = 64, launches: int 
     return _summary(per, 4)
 
 
+def decode_phases(n_keys: int, batch: int = 64, heads: int = 4, d_head: int = 64, launches: int = 12):
+    """TinyGPT's decode attention: one query per (sequence, head) against n_keys cached keys,
+    in the decoder's cache layout (row t*batch + b of [context * batch, 3 * d_model])."""
+    import torch
+
+    from .runtime import mi355x as rt
+    D = heads * d_head
+    g = torch.Generator(device="cuda").manual_seed(n_keys)
+    cache = torch.randn((n_keys * batch, 3 * D), device="cuda", generator=g)
+    att = torch.empty((batch, D), device="cuda")
+    q = cache[(n_keys - 1) * batch:]
+    per = _trace("attention", lambda i: rt.attn_decode(q, cache[:, D:], cache[:, 2 * D:], att, d_head ** -0.5,
+                                                       3 * D, d_head, 3 * D, d_head, batch * 3 * D, 3 * D, d_head,
+                                                       batch * 3 * D, D, d_head, n_keys, batch, heads, d_head),
+                 launches)
+    return _summary(per, 4)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--no-build", action="store_true", help="use the traced library already built")
@@ -140,6 +159,11 @@ def main():
     print(f"| attention 32 x 1024 x 64 causal | {int(m['waves'])} | {us(m['last_wave_start'])} | "
           f"{us(m['first_data'])} (Q staged) | {us(m['wave_wait'])} | {us(m['end'])} | {us(m['gap_to_next'])} | "
           f"per wave: loop {us(m['loop'])}, merge {us(m['merge'])} |")
+    for nk in (96, 160):
+        m = decode_phases(nk)
+        print(f"| decode attention 64 x 4 heads x 64, {nk} keys | {int(m['waves'])} | {us(m['last_wave_start'])} | "
+              f"{us(m['first_data'])} (K, V in) | {us(m['wave_wait'])} | {us(m['end'])} | {us(m['gap_to_next'])} | "
+              f"per wave: scores and max {us(m['loop'])}, exp, sum, P V {us(m['merge'])} |")
 
 
 if __name__ == "__main__":

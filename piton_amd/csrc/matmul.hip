@@ -18,6 +18,8 @@
 //     so the stored elements equal sum_k A[m,k] B[k,n] exactly as the reference's masks give;
 //   * tile order: workgroups renumbered so each XCD gets a contiguous run of logical ids,
 //     then the reference's GROUP_SIZE_M grouping (kernels.py:28-36) on those ids.
+#include <type_traits>
+
 #include "common.h"
 
 namespace piton {
@@ -346,7 +348,12 @@ constexpr int DBM = 64 * DMB, DBN = 64 * DNB;                           // workg
 // tile's loads are interleaved with this tile's products, one after each MFMA, as in the split
 // kernel (2048^3: 163 -> 141 us). With several workgroups per CU the other waves hide the loads
 // and the interleave only slows the wave down (4096^3: 1.02 -> 1.42 ms), so it is off there.
-template <bool ONE_GEN>
+// AKC / BKC: A / B is contiguous along K (A row-major, B column-major). A K-contiguous operand
+// is read as float4 chunks along k (lane half h holds k = 16 h + s for s = 0..15); an M- or
+// N-contiguous one one element per k, coalesced across the lanes' 32 consecutive rows or
+// columns. Either way lane (h, l31) supplies the same k at step s, so every layout runs the same
+// MFMA sequence and gives the same bits.
+template <bool ONE_GEN, bool AKC, bool BKC>
 __global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(ONE_GEN ? 2 : PITON_GEMM_DIRECT_WAVES)))
 void gemm_direct_kernel(GemmArgs g) {
     const int t = threadIdx.x;
@@ -365,35 +372,57 @@ void gemm_direct_kernel(GemmArgs g) {
     const int pid_n = (pid % in_group) / gsize;
     const int64_t m0 = (int64_t)pid_m * DBM, n0 = (int64_t)pid_n * DBN;
 
+    // descriptors bounded at each matrix's last element (whole tiles: every load is inside)
     const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.a), (short)0,
-                                                      (int)((g.M - 1) * g.s_am * 4 + g.K * 4), 0x00020000);
+                                                      (int)(((g.M - 1) * g.s_am + (g.K - 1) * g.s_ak + 1) * 4), 0x00020000);
     const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.b), (short)0,
-                                                      (int)((g.K - 1) * g.s_bk * 4 + g.N * 4), 0x00020000);
+                                                      (int)(((g.K - 1) * g.s_bk + (g.N - 1) * g.s_bn + 1) * 4), 0x00020000);
+    // the contiguous axis has stride 1 (the host checks it): a compile-time constant here
+    const int64_t s_am = AKC ? g.s_am : 1, s_ak = AKC ? 1 : g.s_ak;
+    const int64_t s_bk = BKC ? 1 : g.s_bk, s_bn = BKC ? g.s_bn : 1;
+    // per-lane byte offsets of the block's row (A) or column (B) at the lane half's first k
     uint32_t va[DMB], vb[DNB];
 #pragma unroll
-    for (int i = 0; i < DMB; i++) va[i] = (uint32_t)(((m0 + wm * 32 * DMB + i * 32 + l31) * g.s_am + DKH * half) * 4);
+    for (int i = 0; i < DMB; i++)
+        va[i] = (uint32_t)(((m0 + wm * 32 * DMB + i * 32 + l31) * s_am + (int64_t)(DKH * half) * s_ak) * 4);
 #pragma unroll
     for (int i = 0; i < DNB; i++)
-        vb[i] = (uint32_t)(((int64_t)(DKH * half) * g.s_bk + n0 + wn * 32 * DNB + i * 32 + l31) * 4);
-    const uint32_t sbk4 = (uint32_t)(g.s_bk * 4);
+        vb[i] = (uint32_t)(((int64_t)(DKH * half) * s_bk + (n0 + wn * 32 * DNB + i * 32 + l31) * s_bn) * 4);
+    const uint32_t sak4 = (uint32_t)(s_ak * 4), sbk4 = (uint32_t)(s_bk * 4);
 
+    constexpr int AQ = AKC ? DKH / 4 : DKH, BQ = BKC ? DKH / 4 : DKH;  // loads per block and K tile
     struct Ops {
-        f32x4 a[DMB][DKH / 4];
-        float b[DNB][DKH];
+        std::conditional_t<AKC, f32x4, float> a[DMB][AQ];
+        std::conditional_t<BKC, f32x4, float> b[DNB][BQ];
     };
     auto load = [&](int kt, Ops &o) {
-        const int ka = kt * (DKT * 4);
-        const int kb = (int)((uint32_t)kt * DKT * sbk4);
+        const int ka = (int)((uint32_t)kt * DKT * sak4), kb = (int)((uint32_t)kt * DKT * sbk4);
 #pragma unroll
         for (int i = 0; i < DMB; i++)
 #pragma unroll
-            for (int q = 0; q < DKH / 4; q++)
-                o.a[i][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(va[i] + 16 * q), ka, 0));
+            for (int q = 0; q < AQ; q++) {
+                if constexpr (AKC)
+                    o.a[i][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(va[i] + 16 * q), ka, 0));
+                else
+                    o.a[i][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)va[i], ka + q * (int)sak4, 0));
+            }
 #pragma unroll
-        for (int s = 0; s < DKH; s++)
+        for (int q = 0; q < BQ; q++)
 #pragma unroll
-            for (int i = 0; i < DNB; i++)
-                o.b[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)vb[i], kb + s * (int)sbk4, 0));
+            for (int i = 0; i < DNB; i++) {
+                if constexpr (BKC)
+                    o.b[i][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(vb[i] + 16 * q), kb, 0));
+                else
+                    o.b[i][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)vb[i], kb + q * (int)sbk4, 0));
+            }
+    };
+    auto aval = [](const Ops &o, int i, int s) {
+        if constexpr (AKC) return o.a[i][s >> 2][s & 3];
+        else return o.a[i][s];
+    };
+    auto bval = [](const Ops &o, int j, int s) {
+        if constexpr (BKC) return o.b[j][s >> 2][s & 3];
+        else return o.b[j][s];
     };
     f32x16 acc[DMB][DNB];
 #pragma unroll
@@ -409,14 +438,14 @@ void gemm_direct_kernel(GemmArgs g) {
             for (int i = 0; i < DMB; i++)
 #pragma unroll
                 for (int j = 0; j < DNB; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i][s >> 2][s & 3], o.b[j][s], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(aval(o, i, s), bval(o, j, s), acc[i][j], 0, 0, 0);
     };
     // K % (2 DKT) == 0: the tiles come in pairs. The last pair's prefetch loads the last tile
     // again (never used) rather than a tile past K: every load stays inside the matrices, which
     // also keeps the uniform offsets in `soffset` legal (the descriptor's range check covers the
     // per-lane offset only)
     const int nk = (int)(g.K / DKT);
-    constexpr int DLOADS = DMB * DKH / 4 + DNB * DKH, DMFMAS = DKH * DMB * DNB;
+    constexpr int DLOADS = DMB * AQ + DNB * BQ, DMFMAS = DKH * DMB * DNB;
     auto interleave = [&]() {
         if constexpr (ONE_GEN) {
 #pragma unroll
@@ -938,6 +967,22 @@ static void launch_b(int bl, const GemmArgs &g, int nwg, hipStream_t st) {
     else PITON_LAUNCH((gemm_f32_kernel<A_L, SCALAR, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
 }
 
+// one_gen: no more tiles than CUs; akc / bkc: A / B contiguous along K
+static void launch_direct(bool one_gen, bool akc, bool bkc, const GemmArgs &g, unsigned tiles, hipStream_t st) {
+    const dim3 grid(tiles), block(GTHREADS);
+    if (one_gen) {
+        if (akc && !bkc) PITON_LAUNCH((gemm_direct_kernel<true, true, false>), grid, block, 0, st, g);
+        else if (akc) PITON_LAUNCH((gemm_direct_kernel<true, true, true>), grid, block, 0, st, g);
+        else if (!bkc) PITON_LAUNCH((gemm_direct_kernel<true, false, false>), grid, block, 0, st, g);
+        else PITON_LAUNCH((gemm_direct_kernel<true, false, true>), grid, block, 0, st, g);
+    } else {
+        if (akc && !bkc) PITON_LAUNCH((gemm_direct_kernel<false, true, false>), grid, block, 0, st, g);
+        else if (akc) PITON_LAUNCH((gemm_direct_kernel<false, true, true>), grid, block, 0, st, g);
+        else if (!bkc) PITON_LAUNCH((gemm_direct_kernel<false, false, false>), grid, block, 0, st, g);
+        else PITON_LAUNCH((gemm_direct_kernel<false, false, true>), grid, block, 0, st, g);
+    }
+}
+
 // split_ok: row-major shapes that give the direct kernel fewer 128 x 128 tiles than CUs, or
 // that are not whole tiles, take the split kernel (its k order differs from the LDS kernel's, so
 // the dense entry, whose bits the fused digits chain reproduces, keeps the LDS kernel)
@@ -955,11 +1000,15 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
     const int al = layout_a(g), bl = layout_b(g);
     const int nwg = (int)tiles;
     const bool whole = al == VEC_ROW && bl == VEC_ROW && g.M % GBM == 0 && g.N % GBN == 0 && g.K % GBK == 0 && g.K > 0;
-    // the direct kernel addresses rows by 32-bit byte offsets from the matrix base: positive row
-    // strides and every element within 2^31 bytes
-    const bool direct = PITON_GEMM_DIRECT && whole && g.M % DBM == 0 && g.N % DBN == 0 && g.K % (2 * DKT) == 0 &&
-                        g.s_am > 0 && g.s_bk > 0 && (g.M - 1) * g.s_am + g.K < (1LL << 29) &&
-                        (g.K - 1) * g.s_bk + g.N < (1LL << 29);
+    // the direct kernel takes either layout of each operand (row- or column-major, 16-byte
+    // vectors along the contiguous axis) with whole tiles; it addresses elements by 32-bit byte
+    // offsets from the matrix base: positive strides and every element within 2^31 bytes
+    const bool vec_layouts = (al == VEC_ROW || al == VEC_COL) && (bl == VEC_ROW || bl == VEC_COL);
+    const bool direct = PITON_GEMM_DIRECT && vec_layouts && g.K > 0 && g.M % DBM == 0 && g.N % DBN == 0 &&
+                        g.K % (2 * DKT) == 0 && g.s_am > 0 && g.s_ak > 0 && g.s_bk > 0 && g.s_bn > 0 &&
+                        (g.M - 1) * g.s_am + (g.K - 1) * g.s_ak < (1LL << 29) &&
+                        (g.K - 1) * g.s_bk + (g.N - 1) * g.s_bn < (1LL << 29);
+    const bool akc = al == VEC_ROW, bkc = bl == VEC_COL;  // the operands contiguous along K
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const SplitPlan sp =
         split_ok && !(direct && tiles >= PITON_DIRECT_TILES_PER_CU * cus) ? plan_split(g, cus) : SplitPlan{0, 0, 0};
@@ -971,10 +1020,8 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
         const bool avec = g.s_am % 4 == 0 && g.K % 4 == 0 && aligned16(g.a);
         if (sp.nb == 2) launch_split_nb<2>(gs, sp.ks, avec, (unsigned)sp.tiles, st);
         else launch_split_nb<1>(gs, sp.ks, avec, (unsigned)sp.tiles, st);
-    } else if (direct && tiles <= cus) {
-        PITON_LAUNCH(gemm_direct_kernel<true>, dim3((unsigned)tiles), dim3(GTHREADS), 0, st, g);
     } else if (direct) {
-        PITON_LAUNCH(gemm_direct_kernel<false>, dim3((unsigned)tiles), dim3(GTHREADS), 0, st, g);
+        launch_direct(tiles <= cus, akc, bkc, g, (unsigned)tiles, st);
     } else if (whole)
         PITON_LAUNCH((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);
     else if (al == VEC_ROW) launch_b<VEC_ROW>(bl, g, nwg, st);

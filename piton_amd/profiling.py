@@ -28,7 +28,7 @@ CAL_WRITE = 64 * 2 ** 20 * 4
 # benchmark launches, identified by kernel name prefix and Grid_Size_X (work-items):
 # (workload, algorithmic HBM bytes per launch, algorithmic FLOPs per launch)
 BENCH = {
-    ("gemm_direct_kernel<false>", 262144): ("matmul 4096^3", 3 * 4096 * 4096 * 4, 2 * 4096 ** 3),
+    ("gemm_direct_kernel<false, true, false>", 262144): ("matmul 4096^3", 3 * 4096 * 4096 * 4, 2 * 4096 ** 3),
     ("softmax_rows_kernel<4, true>", 262144): ("softmax 4096 x 1024", 2 * 4 * 4096 * 1024, None),
     ("softmax_wg_kernel<2, 512, true>", 2097152): ("softmax 4096 x 4096", 2 * 4 * 4096 * 4096, None),
     ("softmax_rows_kernel<8, false>", 196608): ("softmax 4096 x 1823", 2 * 4 * 4096 * 1823, None),

@@ -206,6 +206,44 @@ def test_seeded_shape_sweep_against_float64():
         assert not bad.any(), (case, M, N, K, pad_a, pad_b, int(bad.sum()))
 
 
+LAYOUTS = ["row-major", "A transposed", "B transposed", "both transposed"]
+
+
+def _stored(x, transposed):
+    """x (rows x cols) on the GPU, row-major or stored transposed (element (r, c) at c * rows + r)."""
+    if transposed:
+        return torch.from_numpy(np.ascontiguousarray(x.T)).cuda().t()
+    return torch.from_numpy(x).cuda()
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 384, 192), (2048, 4096, 128)])
+def test_transposed_operands_take_the_direct_kernel(M, N, K):
+    """Whole 128 x 128 tiles with K % 64 == 0 go to the register-direct kernel in every layout of
+    A and B (row- or column-major). Each lane supplies the same k at each MFMA step whichever
+    operand is contiguous, so the layouts that take it give identical bits (row-major shapes with
+    fewer tiles than CUs take the split kernel instead); all stay within the float32 bound."""
+    rng = np.random.default_rng(M + N + K)
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    ref = fp64.matmul(a, b)
+    bound = (K + 2) * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+    out, kernels = {}, {}
+    for i, name in enumerate(LAYOUTS):
+        A, B = _stored(a, i & 1), _stored(b, i & 2)
+        C = torch.full((M, N), -1.0, device="cuda")
+        rt.matmul(A, B, C, M, N, K, A.stride(0), A.stride(1), B.stride(0), B.stride(1), N, 1)
+        kernels[name] = rt.last_launches()[0]["kernel"]
+        torch.cuda.synchronize()
+        out[name] = C.cpu().numpy()
+        assert not (np.abs(out[name] - ref) > bound).any(), name
+    for name in LAYOUTS[1:]:
+        assert kernels[name].startswith("gemm_direct_kernel"), (name, kernels[name])
+    direct = [n for n in LAYOUTS if kernels[n].startswith("gemm_direct_kernel")]
+    assert len(direct) == (4 if M * N >= 256 * 128 * 128 else 3), kernels
+    for name in direct[1:]:
+        np.testing.assert_array_equal(out[name], out[direct[0]], err_msg=name)
+
+
 @pytest.mark.parametrize("K", [128, 96])
 def test_negative_row_stride_through_the_c_abi(K):
     """The C entry takes any strides: A addressed from its last row with row stride -K (a

@@ -7,7 +7,7 @@ import pytest
 
 from piton_amd import profiling
 
-GEMM = "void piton::gemm_direct_kernel<false>(piton::GemmArgs)"
+GEMM = "void piton::gemm_direct_kernel<false, true, false>(piton::GemmArgs)"
 ADD = "void piton::add_vec4_kernel(float const*, float const*, float*, long)"
 COLS = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value", "Start_Timestamp",
         "End_Timestamp"]

@@ -205,25 +205,28 @@ def bench_matmul(n, steps, warmup):
                 kernel=rec.last_stats["launches"][0]["kernel"])
 
 
-def bench_matmul_shape(M, N, K, lda, ldb, ldc, launches=32):
-    """Config 2's other shapes (HIP-graph replays, back to back): TFLOP/s and MFMA fraction."""
+def bench_matmul_shape(M, N, K, lda, ldb, ldc, launches=32, b_transposed=False):
+    """Config 2's other shapes (HIP-graph replays, back to back): TFLOP/s and MFMA fraction.
+    b_transposed: B stored column-major (stride_bk = 1, stride_bn = ldb)."""
     import torch
 
     from piton_amd.runtime import mi355x as rt
     g = torch.Generator(device="cuda").manual_seed(M + N + K)
     A = torch.rand((M, lda), device="cuda", generator=g) * 2 - 1
-    B = torch.rand((K, ldb), device="cuda", generator=g) * 2 - 1
+    B = torch.rand((N, ldb) if b_transposed else (K, ldb), device="cuda", generator=g) * 2 - 1
     C = torch.empty((M, ldc), device="cuda")
+    s_bk, s_bn = (1, ldb) if b_transposed else (ldb, 1)
 
     def step(_i):
-        rt.matmul(A, B, C, M, N, K, lda, 1, ldb, 1, ldc, 1, 8)
+        rt.matmul(A, B, C, M, N, K, lda, 1, s_bk, s_bn, ldc, 1, 8)
 
     step(0)
     kernel = rt.last_launches()[0]["kernel"]
     avg = timed_graph(step, launches)
     flops = 2.0 * M * N * K
-    return dict(M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, kernel=kernel, us=round(avg * 1e6, 3),
-                tflops=round(flops / avg / 1e12, 3), frac_mfma=round(flops / avg / PEAK_FP32_MFMA, 4))
+    return dict(M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, b_transposed=b_transposed, kernel=kernel,
+                us=round(avg * 1e6, 3), tflops=round(flops / avg / 1e12, 3),
+                frac_mfma=round(flops / avg / PEAK_FP32_MFMA, 4))
 
 
 def bench_softmax(n, rows=4096, launches=48, sample_rows=256):
@@ -603,7 +606,9 @@ def main():
     samples = {}
     if not args.no_extras:
         line["matmul_shapes"] = [bench_matmul_shape(s, s, s, s, s, s) for s in (512, 1024)] + \
-            [bench_matmul_shape(1000, 1800, 700, 703, 1805, 1807)]
+            [bench_matmul_shape(1000, 1800, 700, 703, 1805, 1807)] + \
+            [bench_matmul_shape(s, s, s, s, s, s, launches=8 if s == 4096 else 32, b_transposed=True)
+             for s in (1024, 4096)]
         line["softmax"] = []
         for nc in (1024, 4096, 1823):
             sm, samples[f"softmax {nc}"] = bench_softmax(nc)

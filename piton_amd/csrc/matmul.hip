@@ -486,21 +486,27 @@ void gemm_direct_kernel(GemmArgs g) {
         }
 }
 
-// Row-major shapes with too few 128 x 128 tiles to fill the chip (config 2's 512^3 has 16 and
-// 1024^3 64 for 256 CUs) or with ragged edges: a workgroup owns a TB x TB tile (TB = 32 NB) and
+// Shapes with too few 128 x 128 tiles to fill the chip (config 2's 512^3 has 16 and 1024^3 64
+// for 256 CUs) or with ragged edges: a workgroup owns a TB x TB tile (TB = 32 NB) and
 // its KS waves split K, each wave computing the whole tile, NB x NB blocks of
 // v_mfma_f32_32x32x2_f32, over the K tiles kt = wave, wave + KS, ... (interleaved, so the waves
 // read neighbouring k together). Operands go from memory straight into registers as in the
 // direct kernel (the same k order inside a K tile of 32: lane half h supplies k = 16 h + s at
-// step s), through buffer descriptors bounded at each matrix's last element: rows of A past M
-// and rows of B past K read as zeros, and the K tail of A (k >= K inside the last tile, which
-// may hold padding or the next row) is zeroed before its products, as the reference's K mask
-// does. The KS partial tiles meet in LDS and add in wave order (fixed: the result does not
-// depend on timing); the epilogue (bias, ReLU, residual) then stores rows < M and columns < N.
-// AVEC: A rows 16-byte aligned (16-byte loads of A). Otherwise each lane's 16 consecutive A
-// values sit r = (row start) mod 4 floats past a 16-byte boundary, the same r for every K tile:
-// the lane loads the five aligned 16-byte chunks that cover them and picks the four-way shift in
-// registers (5 loads and about 50 selects per block instead of 16 loads).
+// step s), through buffer descriptors bounded at each matrix's last element. The K tail (k >= K
+// inside the last tile, which may hold padding or the next row or column) reads as zeros, as the
+// reference's K mask makes it: a row-major A's elements there, and a column-major B's, take an
+// offset past the bound; a column-major A's (columns at least M floats apart) and a row-major
+// B's rows past K lie past the bound already. Rows of A past M and columns of B past N feed only
+// rows and columns of C that are not stored. The KS partial tiles meet in LDS and add in wave
+// order (fixed: the result does not depend on timing); the epilogue (bias, ReLU, residual) then
+// stores rows < M and columns < N.
+// AM: A's layout. A_ROW16: row-major, rows 16-byte aligned (16-byte loads along k). A_ROW:
+// row-major, each lane's 16 consecutive A values sit r = (row start) mod 4 floats past a 16-byte
+// boundary, the same r for every K tile: the lane loads the five aligned 16-byte chunks that
+// cover them and picks the four-way shift in registers (5 loads and about 50 selects per block
+// instead of 16 loads). A_COL: column-major (stride 1 along M), one float per k, coalesced over
+// the lanes' 32 rows. BKC: B column-major (stride 1 along K, 16-byte aligned, K % 4 == 0),
+// 16-byte loads along k; otherwise B has stride 1 along N and loads one float per k.
 #ifndef PITON_SPLIT_MAX_WAVES
 #define PITON_SPLIT_MAX_WAVES 4
 #endif
@@ -512,9 +518,11 @@ void gemm_direct_kernel(GemmArgs g) {
 #define PITON_DIRECT_TILES_PER_CU 1
 #endif
 constexpr int kMaxSplitWaves = PITON_SPLIT_MAX_WAVES;
+enum SplitA { A_ROW16 = 0, A_ROW = 1, A_COL = 2 };
 
-template <int NB, int KS, bool AVEC>
+template <int NB, int KS, int AM, bool BKC>
 __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
+    constexpr bool AVEC = AM == A_ROW16;
     constexpr int TB = 32 * NB;
     constexpr int NACC = NB * NB * 16;  // accumulator registers per lane
     __shared__ float red[KS > 1 ? KS : 1][NACC][64];
@@ -533,46 +541,56 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     const int pid_n = (pid % in_group) / gsize;
     const int64_t m0 = (int64_t)pid_m * TB, n0 = (int64_t)pid_n * TB;
 
-    // bounded at the last element of each matrix: offsets at or past the bound read as zero. A's
-    // descriptor starts at the 16-byte boundary at or below A (inside A's allocation, whose start
-    // is aligned) and its bound is rounded up to whole 16-byte chunks (the last chunk lies in the
-    // page of A's last element), so a 16-byte load is either wholly inside or wholly outside.
-    const int off0 = (int)((reinterpret_cast<uintptr_t>(g.a) >> 2) & 3);  // A's first float past the boundary
+    // the stride along each operand's contiguous axis is 1 (the host checks it)
+    const int64_t s_am = AM == A_COL ? 1 : g.s_am, s_ak = AM == A_COL ? g.s_ak : 1;
+    const int64_t s_bk = BKC ? 1 : g.s_bk, s_bn = BKC ? g.s_bn : 1;
+    // bounded at the last element of each matrix: offsets at or past the bound read as zero. A
+    // row-major A's descriptor starts at the 16-byte boundary at or below A (inside A's
+    // allocation, whose start is aligned) and its bound is rounded up to whole 16-byte chunks (the
+    // last chunk lies in the page of A's last element), so a 16-byte load is either wholly inside
+    // or wholly outside.
+    const int off0 = AM == A_COL ? 0 : (int)((reinterpret_cast<uintptr_t>(g.a) >> 2) & 3);  // A's first float past the boundary
     const float *a_al = g.a - off0;
-    const int64_t a_end = off0 + (g.M - 1) * g.s_am + g.K;                  // floats from a_al
+    const int64_t a_end = off0 + (g.M - 1) * s_am + (g.K - 1) * s_ak + 1;  // floats from a_al
     const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a_al), (short)0,
                                                       (int)(((a_end + 3) & ~(int64_t)3) * 4), 0x00020000);
     const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.b), (short)0,
-                                                      (int)(((g.K - 1) * g.s_bk + g.N) * 4), 0x00020000);
+                                                      (int)(((g.K - 1) * s_bk + (g.N - 1) * s_bn + 1) * 4), 0x00020000);
     uint32_t va[NB], vb[NB];
-    int ra_shift[NB];  // !AVEC: this lane's row start past its 16-byte boundary, in floats
+    int ra_shift[NB];  // A_ROW: this lane's row start past its 16-byte boundary, in floats
 #pragma unroll
     for (int i = 0; i < NB; i++) {
-        const int64_t e0 = off0 + (m0 + i * 32 + l31) * g.s_am + 16 * half;
+        const int64_t e0 = off0 + (m0 + i * 32 + l31) * s_am + 16 * half * s_ak;
         ra_shift[i] = (int)(e0 & 3);
-        va[i] = (uint32_t)((e0 & ~(int64_t)3) * 4);
+        va[i] = (uint32_t)((AM == A_COL ? e0 : e0 & ~(int64_t)3) * 4);
     }
 #pragma unroll
-    for (int j = 0; j < NB; j++) vb[j] = (uint32_t)(((int64_t)(16 * half) * g.s_bk + n0 + j * 32 + l31) * 4);
-    const uint32_t sbk4 = (uint32_t)(g.s_bk * 4);
+    for (int j = 0; j < NB; j++) vb[j] = (uint32_t)(((int64_t)(16 * half) * s_bk + (n0 + j * 32 + l31) * s_bn) * 4);
+    const uint32_t sak4 = (uint32_t)(s_ak * 4), sbk4 = (uint32_t)(s_bk * 4);
     const int nk = (int)((g.K + 31) / 32);
 
-    constexpr int AW = AVEC ? 16 : 20;  // A floats a lane loads per block and tile
+    constexpr int AW = AM == A_ROW ? 20 : 16;  // A floats a lane loads per block and tile
     struct Ops {
         float a[NB][AW];
         float b[NB][16];
     };
     // every offset goes in the per-lane address, which is what the descriptor's range check
-    // covers. The K tail: a lane's A elements with k >= K get an offset past the bound (2^31,
-    // beyond any bound of a matrix under 2 GiB), so they read as zero with no data dependence;
-    // B's rows past K are past its bound already.
+    // covers. The K tail: a row-major A's elements and a column-major B's with k >= K get an
+    // offset past the bound (2^31, beyond any bound of a matrix under 2 GiB), so they read as zero
+    // with no data dependence; a column-major A's and a row-major B's lie past the bound already.
     constexpr uint32_t kOut = 0x80000000u;
     auto load = [&](int kt, Ops &o) {
-        const uint32_t ka = (uint32_t)kt * 128u, kb = (uint32_t)kt * 32u * sbk4;
+        const uint32_t ka = (uint32_t)kt * 32u * sak4, kb = (uint32_t)kt * 32u * sbk4;
         const int64_t k0 = (int64_t)kt * 32 + 16 * half;  // this lane's first k of the tile
 #pragma unroll
         for (int i = 0; i < NB; i++) {
-            if constexpr (AVEC) {
+            if constexpr (AM == A_COL) {
+                // columns no closer than M floats apart (the host checks it): (m, k) with k >= K
+                // lies at or past (K - 1) s_ak + M, the bound
+#pragma unroll
+                for (int s = 0; s < 16; s++)
+                    o.a[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)(va[i] + ka + s * sak4), 0, 0));
+            } else if constexpr (AVEC) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const uint32_t off = k0 + 4 * q < g.K ? va[i] + ka + 16 * q : kOut;
@@ -591,11 +609,23 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
                 }
             }
         }
-#pragma unroll
-        for (int s = 0; s < 16; s++)
+        if constexpr (BKC) {
 #pragma unroll
             for (int j = 0; j < NB; j++)
-                o.b[j][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)(vb[j] + kb + s * sbk4), 0, 0));
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t off = k0 + 4 * q < g.K ? vb[j] + kb + 16 * q : kOut;
+                    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o.b[j][4 * q + e] = v[e];
+                }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 16; s++)
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+                    o.b[j][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)(vb[j] + kb + s * sbk4), 0, 0));
+        }
     };
     f32x16 acc[NB][NB];
 #pragma unroll
@@ -604,9 +634,9 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
         for (int j = 0; j < NB; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-    // !AVEC: the lane's 16 values of block i: window[s + r], zero where k0 + s >= K
+    // A_ROW: the lane's 16 values of block i: window[s + r], zero where k0 + s >= K
     auto a_vals = [&](const Ops &o, int i, int kt, float (&v)[16]) {
-        if constexpr (AVEC) {
+        if constexpr (AM != A_ROW) {
 #pragma unroll
             for (int s = 0; s < 16; s++) v[s] = o.a[i][s];
         } else {
@@ -655,7 +685,8 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
 #ifndef PITON_SPLIT_LPM
 #define PITON_SPLIT_LPM 1
 #endif
-    constexpr int LOADS = NB * (AVEC ? 4 : 5) + NB * 16, MFMAS = 16 * NB * NB, LPM = PITON_SPLIT_LPM;
+    constexpr int LOADS = NB * (AM == A_ROW16 ? 4 : AM == A_ROW ? 5 : 16) + NB * (BKC ? 4 : 16);
+    constexpr int MFMAS = 16 * NB * NB, LPM = PITON_SPLIT_LPM;
     auto interleave = [&]() {
 #pragma unroll
         for (int i = 0; i < MFMAS; i++) {
@@ -914,18 +945,29 @@ static int layout_b(const GemmArgs &g) {
     return SCALAR;
 }
 
-// The split kernel's tile (NB blocks of 32 per side) and waves per workgroup for a row-major
-// shape, or nb = 0 when it does not apply. Tiles of 64 when there are at least as many as
+// The split kernel's tile (NB blocks of 32 per side), waves per workgroup and operand layouts
+// for a shape, or nb = 0 when it does not apply. Tiles of 64 when there are at least as many as
 // CUs, else of 32; then the waves double (up to kMaxSplitWaves) until the launch has
 // PITON_SPLIT_WAVES_PER_CU waves per CU, as long as each wave keeps at least two K tiles
 // (8 per CU: 1536^3 103 -> 88 us against 4; the other shapes measured the same).
 struct SplitPlan {
     int nb, ks;
     int64_t tiles;
+    int am;    // SplitA: A's layout
+    bool bkc;  // B column-major
 };
 static SplitPlan plan_split(const GemmArgs &g, int cus) {
-    SplitPlan p{0, 0, 0};
-    if (g.s_ak != 1 || g.s_bn != 1 || g.s_am <= 0 || g.s_bk <= 0 || g.K <= 0 || g.M <= 0 || g.N <= 0) return p;
+    SplitPlan p{0, 0, 0, A_ROW16, false};
+    if (g.K <= 0 || g.M <= 0 || g.N <= 0) return p;
+    // A with stride 1 along K (16-byte loads where its rows are 16-byte aligned and K % 4 == 0) or
+    // along M with columns at least M floats apart; B with stride 1 along N, or along K with
+    // 16-byte aligned columns and K % 4 == 0
+    if (g.s_ak == 1 && g.s_am > 0) p.am = g.s_am % 4 == 0 && g.K % 4 == 0 && aligned16(g.a) ? A_ROW16 : A_ROW;
+    else if (g.s_am == 1 && g.s_ak >= g.M) p.am = A_COL;
+    else return p;
+    if (g.s_bn == 1 && g.s_bk > 0) p.bkc = false;
+    else if (g.s_bk == 1 && g.s_bn > 0 && g.s_bn % 4 == 0 && g.K % 4 == 0 && aligned16(g.b)) p.bkc = true;
+    else return p;
     auto tiles = [&](int64_t tb) { return ((g.M + tb - 1) / tb) * ((g.N + tb - 1) / tb); };
     const int64_t nk = (g.K + 31) / 32;
 #ifndef PITON_SPLIT_NB_MAX
@@ -937,27 +979,32 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     while (ks < kMaxSplitWaves && nt * ks < PITON_SPLIT_WAVES_PER_CU * (int64_t)cus && 4 * ks <= nk) ks *= 2;
     // every byte offset a lane forms (the prefetch past the last tile included) stays below 2^31
     const int64_t tb = 32 * nb, kpad = g.K + 32 * (2 * ks + 3);  // the farthest prefetch: tile nk - 1 + 2 ks
-    if (((g.M + tb) * g.s_am + kpad) * 4 >= (1LL << 31) || (kpad * g.s_bk + g.N + tb) * 4 >= (1LL << 31) ||
-        nt > 0x7FFFFFFF)
+    if (((g.M + tb) * g.s_am + kpad * g.s_ak + 4) * 4 >= (1LL << 31) ||
+        (kpad * g.s_bk + (g.N + tb) * g.s_bn) * 4 >= (1LL << 31) || nt > 0x7FFFFFFF)
         return p;
     p.nb = nb, p.ks = ks, p.tiles = nt;
     return p;
 }
 
 template <int NB, int KS>
-static void launch_split_ks(const GemmArgs &g, bool avec, unsigned nwg, hipStream_t st) {
-    if (avec) PITON_LAUNCH((gemm_split_kernel<NB, KS, true>), dim3(nwg), dim3(64 * KS), 0, st, g);
-    else PITON_LAUNCH((gemm_split_kernel<NB, KS, false>), dim3(nwg), dim3(64 * KS), 0, st, g);
+static void launch_split_ks(const GemmArgs &g, int am, bool bkc, unsigned nwg, hipStream_t st) {
+    const dim3 grid(nwg), block(64 * KS);
+    if (am == A_ROW16 && !bkc) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_ROW16, false>), grid, block, 0, st, g);
+    else if (am == A_ROW16) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_ROW16, true>), grid, block, 0, st, g);
+    else if (am == A_ROW && !bkc) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_ROW, false>), grid, block, 0, st, g);
+    else if (am == A_ROW) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_ROW, true>), grid, block, 0, st, g);
+    else if (!bkc) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_COL, false>), grid, block, 0, st, g);
+    else PITON_LAUNCH((gemm_split_kernel<NB, KS, A_COL, true>), grid, block, 0, st, g);
 }
 
 template <int NB>
-static void launch_split_nb(const GemmArgs &g, int ks, bool avec, unsigned nwg, hipStream_t st) {
-    if (ks == 1) launch_split_ks<NB, 1>(g, avec, nwg, st);
-    else if (ks == 2) launch_split_ks<NB, 2>(g, avec, nwg, st);
+static void launch_split_nb(const GemmArgs &g, const SplitPlan &sp, unsigned nwg, hipStream_t st) {
+    if (sp.ks == 1) launch_split_ks<NB, 1>(g, sp.am, sp.bkc, nwg, st);
+    else if (sp.ks == 2) launch_split_ks<NB, 2>(g, sp.am, sp.bkc, nwg, st);
 #if PITON_SPLIT_MAX_WAVES > 4
-    else if (ks == 8) launch_split_ks<NB, 8>(g, avec, nwg, st);
+    else if (sp.ks == 8) launch_split_ks<NB, 8>(g, sp.am, sp.bkc, nwg, st);
 #endif
-    else launch_split_ks<NB, 4>(g, avec, nwg, st);
+    else launch_split_ks<NB, 4>(g, sp.am, sp.bkc, nwg, st);
 }
 
 template <int A_L>
@@ -983,8 +1030,8 @@ static void launch_direct(bool one_gen, bool akc, bool bkc, const GemmArgs &g, u
     }
 }
 
-// split_ok: row-major shapes that give the direct kernel fewer 128 x 128 tiles than CUs, or
-// that are not whole tiles, take the split kernel (its k order differs from the LDS kernel's, so
+// split_ok: shapes that give the direct kernel fewer 128 x 128 tiles than CUs, or that are not
+// whole tiles, take the split kernel when each operand has stride 1 along one axis (its k order differs from the LDS kernel's, so
 // the dense entry, whose bits the fused digits chain reproduces, keeps the LDS kernel)
 static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_ok) {
     if (g.M == 0 || g.N == 0) return PITON_OK;
@@ -1017,9 +1064,8 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
         const int64_t rows = (g.M + 32 * sp.nb - 1) / (32 * sp.nb);
         GemmArgs gs = g;
         gs.group_m = (int)(group_user > rows ? rows : group_user);
-        const bool avec = g.s_am % 4 == 0 && g.K % 4 == 0 && aligned16(g.a);
-        if (sp.nb == 2) launch_split_nb<2>(gs, sp.ks, avec, (unsigned)sp.tiles, st);
-        else launch_split_nb<1>(gs, sp.ks, avec, (unsigned)sp.tiles, st);
+        if (sp.nb == 2) launch_split_nb<2>(gs, sp, (unsigned)sp.tiles, st);
+        else launch_split_nb<1>(gs, sp, (unsigned)sp.tiles, st);
     } else if (direct) {
         launch_direct(tiles <= cus, akc, bkc, g, (unsigned)tiles, st);
     } else if (whole)

@@ -126,10 +126,10 @@ def test_numpy_arrays_copy_in_copy_out():
                                        (256, 384, 128, (4, 8, 3)), (128, 128, 64, (0, 0, 0)),
                                        (384, 256, 2112, (8, 4, 1))])
 def test_whole_tile_shapes_with_padded_rows(M, N, K, pad):
-    """Shapes whose tiles are all whole (M, N multiples of 128) take the unguarded kernels: the
-    register-direct one for K % 64 == 0, whose last prefetch reads past K, and the LDS one's
-    whole-tile instantiation for K % 32 == 0. Padded row strides of A, B and C (NaN in the
-    padding) must not leak into the product or past C's rows."""
+    """Shapes whose tiles are all whole (M, N multiples of 128): the register-direct kernel for
+    K % 64 == 0 with at least as many tiles as CUs (its last prefetch reloads the last K tile),
+    the split kernel otherwise. Padded row strides of A, B and C (NaN in the padding) must not
+    leak into the product or past C's rows."""
     rng = np.random.default_rng(M + N + K)
     a = dyadic(rng, (M, K))
     b = dyadic(rng, (K, N))
@@ -216,32 +216,69 @@ def _stored(x, transposed):
     return torch.from_numpy(x).cuda()
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 384, 192), (2048, 4096, 128)])
-def test_transposed_operands_take_the_direct_kernel(M, N, K):
-    """Whole 128 x 128 tiles with K % 64 == 0 go to the register-direct kernel in every layout of
-    A and B (row- or column-major). Each lane supplies the same k at each MFMA step whichever
-    operand is contiguous, so the layouts that take it give identical bits (row-major shapes with
-    fewer tiles than CUs take the split kernel instead); all stay within the float32 bound."""
+@pytest.mark.parametrize("M,N,K,family", [(256, 384, 192, "gemm_split_kernel"),
+                                          (2048, 4096, 128, "gemm_direct_kernel")])
+def test_every_layout_gives_the_same_bits(M, N, K, family):
+    """Row- or column-major A and B: the register-direct kernel (whole 128 x 128 tiles, K % 64 ==
+    0, at least as many tiles as CUs) and the split kernel (fewer tiles) take every layout, and
+    each lane supplies the same k at each MFMA step whichever operand is contiguous, so all four
+    layouts give identical bits, within the float32 bound of the float64 product."""
     rng = np.random.default_rng(M + N + K)
     a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
     b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
     ref = fp64.matmul(a, b)
     bound = (K + 2) * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
-    out, kernels = {}, {}
+    out = {}
     for i, name in enumerate(LAYOUTS):
         A, B = _stored(a, i & 1), _stored(b, i & 2)
         C = torch.full((M, N), -1.0, device="cuda")
         rt.matmul(A, B, C, M, N, K, A.stride(0), A.stride(1), B.stride(0), B.stride(1), N, 1)
-        kernels[name] = rt.last_launches()[0]["kernel"]
+        kernel = rt.last_launches()[0]["kernel"]
         torch.cuda.synchronize()
         out[name] = C.cpu().numpy()
+        assert kernel.startswith(family), (name, kernel)
         assert not (np.abs(out[name] - ref) > bound).any(), name
     for name in LAYOUTS[1:]:
-        assert kernels[name].startswith("gemm_direct_kernel"), (name, kernels[name])
-    direct = [n for n in LAYOUTS if kernels[n].startswith("gemm_direct_kernel")]
-    assert len(direct) == (4 if M * N >= 256 * 128 * 128 else 3), kernels
-    for name in direct[1:]:
-        np.testing.assert_array_equal(out[name], out[direct[0]], err_msg=name)
+        np.testing.assert_array_equal(out[name], out[LAYOUTS[0]], err_msg=name)
+
+
+def _nan_padded(x, transposed, pad):
+    """x (rows x cols) on the GPU in storage whose padding holds NaN: row-major with rows of
+    cols + pad floats, or stored transposed with columns of rows + pad floats."""
+    r, c = x.shape
+    if transposed:
+        full = torch.full((c, r + pad), float("nan"), device="cuda")
+        full[:, :r] = torch.from_numpy(np.ascontiguousarray(x.T)).cuda()
+        return full[:, :r].t()
+    full = torch.full((r, c + pad), float("nan"), device="cuda")
+    full[:, :c] = torch.from_numpy(x).cuda()
+    return full[:, :c]
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 1800, 700), (100, 72, 36), (129, 257, 516), (256, 256, 64)])
+def test_split_kernel_layouts_with_nan_padding(M, N, K):
+    """Shapes that give the direct kernel too few tiles, or ragged edges, take the split kernel in
+    every layout of A and B; the K tail (k >= K inside the last tile of 32) reads as zero, so
+    NaN in the storage's padding, which a tail load of an unmasked operand would read, never
+    reaches C. Every element within the float32 bound of the float64 product."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    ref = fp64.matmul(a, b)
+    bound = (K + 2) * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+    for i, name in enumerate(LAYOUTS):
+        for pad in (0, 4, 3):
+            if pad == 3 and i & 2:
+                continue  # a column-major B is loaded in 16-byte chunks: columns 16-byte aligned
+            A, B = _nan_padded(a, i & 1, pad), _nan_padded(b, i & 2, pad)
+            C = torch.full((M, N), -1.0, device="cuda")
+            rt.matmul(A, B, C, M, N, K, A.stride(0), A.stride(1), B.stride(0), B.stride(1), N, 1)
+            kernel = rt.last_launches()[0]["kernel"]
+            torch.cuda.synchronize()
+            got = C.cpu().numpy()
+            assert kernel.startswith("gemm_split_kernel"), (name, pad, kernel)
+            assert np.isfinite(got).all(), (name, pad, kernel)
+            assert not (np.abs(got - ref) > bound).any(), (name, pad, kernel)
 
 
 @pytest.mark.parametrize("K", [128, 96])
@@ -346,4 +383,4 @@ def test_split_kernel_unaligned_base_and_rows(a_off, lda):
     (launch,) = rt.last_launches()
     torch.cuda.synchronize()
     np.testing.assert_array_equal(C.cpu().numpy(), a @ b)
-    assert launch["kernel"] == "gemm_split_kernel<NB, KS, false>"
+    assert launch["kernel"] == "gemm_split_kernel<NB, KS, A_ROW, false>"

@@ -202,7 +202,7 @@ def bench_matmul(n, steps, warmup):
     wall = time.perf_counter() - t0
     flops = 2.0 * n * n * n
     return dict(wall=wall, kernel_s=e0.elapsed_time(e1) * 1e-3 / steps, flops=flops, a=a, b=b, c=c,
-                kernel=rec.last_stats["launches"][0]["kernel"])
+                kernel=" + ".join(f"{l['kernel']} x {l['grid'][0]}" for l in rec.last_stats["launches"]))
 
 
 def bench_matmul_shape(M, N, K, lda, ldb, ldc, launches=32, b_transposed=False):
@@ -221,7 +221,7 @@ def bench_matmul_shape(M, N, K, lda, ldb, ldc, launches=32, b_transposed=False):
         rt.matmul(A, B, C, M, N, K, lda, 1, s_bk, s_bn, ldc, 1, 8)
 
     step(0)
-    kernel = rt.last_launches()[0]["kernel"]
+    kernel = " + ".join(f"{l['kernel']} x {l['grid'][0]}" for l in rt.last_launches())
     avg = timed_graph(step, launches)
     flops = 2.0 * M * N * K
     return dict(M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, b_transposed=b_transposed, kernel=kernel,

@@ -45,6 +45,7 @@ struct GemmArgs {
     int64_t s_rm;
     int a_kfast, b_nfast;  // scalar loaders: which index runs fastest across threads
     float ln_eps;          // small-row kernel with LN: rows of A are layer-normalised first
+    int tile0;             // register-direct kernel: the logical id of the launch's first tile
 };
 
 // Loads the A tile (GBM x GBK at m0, k0) into 16 registers per thread.
@@ -363,7 +364,7 @@ void gemm_direct_kernel(GemmArgs g) {
 
     const int num_pid_m = (int)(g.M / DBM);
     const int num_pid_n = (int)(g.N / DBN);
-    const int pid = xcd_logical_id(blockIdx.x, gridDim.x, kXcdCount);
+    const int pid = g.tile0 + xcd_logical_id(blockIdx.x, gridDim.x, kXcdCount);
     const int in_group = g.group_m * num_pid_n;
     const int group_id = pid / in_group;
     const int first_m = group_id * g.group_m;
@@ -514,6 +515,9 @@ void gemm_direct_kernel(GemmArgs g) {
 #define PITON_SPLIT_WAVES_PER_CU 8
 #endif
 // the direct kernel takes whole-tile shapes with at least this many 128 x 128 tiles per CU
+#ifndef PITON_GEMM_TAIL_LAUNCH
+#define PITON_GEMM_TAIL_LAUNCH 1
+#endif
 #ifndef PITON_DIRECT_TILES_PER_CU
 #define PITON_DIRECT_TILES_PER_CU 1
 #endif
@@ -1067,7 +1071,18 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
         if (sp.nb == 2) launch_split_nb<2>(gs, sp, (unsigned)sp.tiles, st);
         else launch_split_nb<1>(gs, sp, (unsigned)sp.tiles, st);
     } else if (direct) {
-        launch_direct(tiles <= cus, akc, bkc, g, (unsigned)tiles, st);
+        // the multi-workgroup kernel runs PITON_GEMM_DIRECT_WAVES workgroups per CU at once; a
+        // last generation of at most one tile per CU would run one wave per SIMD with its loads
+        // unhidden, so those tiles go to a second launch of the one-generation kernel
+        const int64_t slots = (int64_t)PITON_GEMM_DIRECT_WAVES * cus, full = tiles / slots * slots;
+        if (PITON_GEMM_TAIL_LAUNCH && tiles > cus && full > 0 && tiles - full > 0 && tiles - full <= cus) {
+            launch_direct(false, akc, bkc, g, (unsigned)full, st);
+            GemmArgs tail = g;
+            tail.tile0 = (int)full;
+            launch_direct(true, akc, bkc, tail, (unsigned)(tiles - full), st);
+        } else {
+            launch_direct(tiles <= cus, akc, bkc, g, (unsigned)tiles, st);
+        }
     } else if (whole)
         PITON_LAUNCH((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);
     else if (al == VEC_ROW) launch_b<VEC_ROW>(bl, g, nwg, st);

@@ -6,11 +6,12 @@
 KT_DIR holds a `--kernel-trace --stats` run of `python3 bench.py` (*_kernel_trace.csv);
 FETCH_DIR / WRITE_DIR hold `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of
 `python3 bench.py --pmc-probe` (*_counter_collection.csv). Prints a markdown summary: each
-kernel's average duration, and its HBM traffic per launch, each counter scaled by the factor
-that maps the calibration add of known size (bench.py CAL_ELEMS: reads 2 x 256 MiB, writes
-256 MiB) onto its true bytes. --json writes {kernel: {fetch_bytes, write_bytes, ...}}.
+kernel's average duration, each benchmark workload's kernel time per step (the sum over its
+launches), and its HBM traffic per step, each counter scaled by the factor that maps the
+calibration add of known size (bench.py CAL_ELEMS: reads 2 x 256 MiB, writes 256 MiB) onto its
+true bytes. --json writes {workload: {fetch_bytes, write_bytes, ...}}.
 With --mfma, PMC_DIR holds a `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES` run of
-`python3 bench.py --pmc-probe`: the MFMA pipe occupancy of the benchmark's MFMA kernels.
+`python3 bench.py --pmc-probe`: the MFMA pipe occupancy of the benchmark's MFMA workloads.
 """
 from __future__ import annotations
 
@@ -25,16 +26,26 @@ import sys
 CAL_READ = 2 * 64 * 2 ** 20 * 4
 CAL_WRITE = 64 * 2 ** 20 * 4
 
-# benchmark launches, identified by kernel name prefix and Grid_Size_X (work-items):
-# (workload, algorithmic HBM bytes per launch, algorithmic FLOPs per launch)
-BENCH = {
-    ("gemm_direct_kernel<false, true, false>", 262144): ("matmul 4096^3", 3 * 4096 * 4096 * 4, 2 * 4096 ** 3),
-    ("softmax_rows_kernel<4, true>", 262144): ("softmax 4096 x 1024", 2 * 4 * 4096 * 1024, None),
-    ("softmax_wg_kernel<2, 512, true>", 2097152): ("softmax 4096 x 4096", 2 * 4 * 4096 * 4096, None),
-    ("softmax_rows_kernel<8, false>", 196608): ("softmax 4096 x 1823", 2 * 4 * 4096 * 1823, None),
-    ("attn_fwd_fast<64, true>", 131072): ("attention 32 x 1024 x 64 causal", 4 * 32 * 1024 * 64 * 4,
-                                          4 * 1024 * 1024 * 64 * 32 // 2),
+# benchmark workloads: (algorithmic HBM bytes per step, algorithmic FLOPs per step)
+WORKLOADS = {
+    "matmul 4096^3": (3 * 4096 * 4096 * 4, 2 * 4096 ** 3),
+    "softmax 4096 x 1024": (2 * 4 * 4096 * 1024, None),
+    "softmax 4096 x 4096": (2 * 4 * 4096 * 4096, None),
+    "softmax 4096 x 1823": (2 * 4 * 4096 * 1823, None),
+    "attention 32 x 1024 x 64 causal": (4 * 32 * 1024 * 64 * 4, 4 * 1024 * 1024 * 64 * 32 // 2),
 }
+# their launches, identified by kernel name and Grid_Size_X (work-items); a step runs each launch
+# of its workload once (the 4096^3 matmul: three 128 x 128 tiles per CU in the first launch,
+# the last 256 tiles in a second)
+LAUNCHES = {
+    ("gemm_direct_kernel<false, true, false>", 196608): "matmul 4096^3",
+    ("gemm_direct_kernel<true, true, false>", 65536): "matmul 4096^3",
+    ("softmax_rows_kernel<4, true>", 262144): "softmax 4096 x 1024",
+    ("softmax_wg_kernel<2, 512, true>", 2097152): "softmax 4096 x 4096",
+    ("softmax_rows_kernel<8, false>", 196608): "softmax 4096 x 1823",
+    ("attn_fwd_fast<64, true>", 131072): "attention 32 x 1024 x 64 causal",
+}
+TIMED = "matmul 4096^3"  # the workload of bench.py's timed region
 
 
 def short(name: str) -> str:
@@ -52,9 +63,9 @@ def _one(pattern):
 
 def kernel_stats(kt_dir, timed_steps=0):
     """Per (kernel, grid) launch statistics from the per-dispatch trace. With timed_steps, the
-    4096^3 matmul group also reports the average of its last `timed_steps` dispatches in
-    dispatch order: bench.py's timed region (its earlier dispatches are the untimed clock ramp
-    and warm-up)."""
+    launches of the 4096^3 matmul also report the average of their last `timed_steps` dispatches
+    in dispatch order: bench.py's timed region (their earlier dispatches are the untimed clock
+    ramp and warm-up)."""
     groups = {}
     for r in csv.DictReader(open(_one(os.path.join(kt_dir, "*_kernel_trace.csv")))):
         if "piton::" in r["Kernel_Name"]:
@@ -66,12 +77,29 @@ def kernel_stats(kt_dir, timed_steps=0):
         in_order = [d for _, d in sorted(td)]
         d = sorted(in_order)
         row = dict(kernel=k, grid=grid, calls=len(d), avg_ns=sum(d) / len(d), min_ns=d[0],
-                   median_ns=d[len(d) // 2], max_ns=d[-1], workload=BENCH.get((k, grid), ("",))[0])
-        if timed_steps and row["workload"] == "matmul 4096^3" and len(in_order) >= timed_steps:
+                   median_ns=d[len(d) // 2], max_ns=d[-1], workload=LAUNCHES.get((k, grid), ""))
+        if timed_steps and row["workload"] == TIMED and len(in_order) >= timed_steps:
             last = in_order[-timed_steps:]
             row["timed_avg_ns"] = sum(last) / len(last)
         rows.append(row)
     return rows
+
+
+def workload_steps(stats):
+    """Per benchmark workload: its launches' average durations summed (the kernel time of one
+    step, gaps between the launches excluded), the timed region's too where known, and the
+    rate that gives."""
+    out = {}
+    for label, (nbytes, flops) in WORKLOADS.items():
+        rows = [r for r in stats if r["workload"] == label]
+        if not rows:
+            continue
+        step_ns = sum(r["avg_ns"] for r in rows)
+        d = dict(launches=[r["kernel"] for r in rows], step_ns=step_ns, algorithmic_bytes=nbytes, flops=flops)
+        if all("timed_avg_ns" in r for r in rows):
+            d["timed_step_ns"] = sum(r["timed_avg_ns"] for r in rows)
+        out[label] = d
+    return out
 
 
 def counters(pmc_dir, counter):
@@ -85,6 +113,9 @@ def counters(pmc_dir, counter):
 
 
 def summarize(kt_dir, fetch_dir, write_dir, timed_steps=0):
+    """Launch statistics, and per workload its HBM traffic per step: each launch's average
+    counter values summed over the step's launches, each counter scaled by the calibration
+    add's factor."""
     fetch, write = counters(fetch_dir, "FETCH_SIZE"), counters(write_dir, "WRITE_SIZE")
     cal = [k for k in fetch if k[0].startswith("add_vec4_kernel")]
     if not cal:
@@ -92,32 +123,41 @@ def summarize(kt_dir, fetch_dir, write_dir, timed_steps=0):
     f_fetch = CAL_READ / fetch[cal[0]]
     f_write = CAL_WRITE / write[cal[0]]
     traffic = {}
-    for k in fetch:
-        if k in write and k in BENCH:
-            label, algo, _ = BENCH[k]
-            traffic[label] = dict(kernel=k[0], grid=k[1], fetch_bytes=fetch[k] * f_fetch,
-                                  write_bytes=write[k] * f_write,
-                                  traffic_bytes=fetch[k] * f_fetch + write[k] * f_write, algorithmic_bytes=algo)
+    for label, (algo, _) in WORKLOADS.items():
+        keys = [k for k, w in LAUNCHES.items() if w == label and k in fetch and k in write]
+        if not keys:
+            continue
+        fb = sum(fetch[k] for k in keys) * f_fetch
+        wb = sum(write[k] for k in keys) * f_write
+        traffic[label] = dict(kernel=" + ".join(k[0] for k in keys), grid=[k[1] for k in keys], fetch_bytes=fb,
+                              write_bytes=wb, traffic_bytes=fb + wb, algorithmic_bytes=algo)
     return kernel_stats(kt_dir, timed_steps), traffic, f_fetch, f_write
 
 
 def mfma_busy(pmc_dir, xcds=8, simds=1024):
-    """MFMA pipe occupancy per benchmark MFMA kernel from a
+    """MFMA pipe occupancy per benchmark MFMA workload from a
     `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES` run: SQ_VALU_MFMA_BUSY_CYCLES is summed
     over the SIMDs and GRBM_GUI_ACTIVE over the XCDs (both as rocprofv3 reports them), so
     busy = MFMA cycles / (GUI cycles / xcds * simds), a ratio of cycles that does not depend
-    on the clock the kernel ran at."""
+    on the clock the kernel ran at; over all dispatches of a workload's launches (weighted by
+    their cycles)."""
     per = {}
     for r in csv.DictReader(open(_one(os.path.join(pmc_dir, "*_counter_collection.csv")))):
         key = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
-        if key not in BENCH or not BENCH[key][2]:
+        if key not in LAUNCHES or not WORKLOADS[LAUNCHES[key]][1]:
             continue
         per.setdefault((key, r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
     out = {}
     for (key, _), d in per.items():
         if "GRBM_GUI_ACTIVE" in d and "SQ_VALU_MFMA_BUSY_CYCLES" in d:
-            out.setdefault(key, []).append(d["SQ_VALU_MFMA_BUSY_CYCLES"] / (d["GRBM_GUI_ACTIVE"] / xcds * simds))
-    return {BENCH[k][0]: dict(kernel=k[0], dispatches=len(v), mfma_busy=sum(v) / len(v)) for k, v in out.items()}
+            w = out.setdefault(LAUNCHES[key], dict(kernels=[], dispatches=0, busy=0.0, cycles=0.0))
+            if key[0] not in w["kernels"]:
+                w["kernels"].append(key[0])
+            w["dispatches"] += 1
+            w["busy"] += d["SQ_VALU_MFMA_BUSY_CYCLES"]
+            w["cycles"] += d["GRBM_GUI_ACTIVE"] / xcds * simds
+    return {label: dict(kernel=" + ".join(w["kernels"]), dispatches=w["dispatches"], mfma_busy=w["busy"] / w["cycles"])
+            for label, w in out.items()}
 
 
 def main(argv=None):
@@ -138,27 +178,29 @@ def main(argv=None):
             sys.stdout.write(f"| {label} | `{m['kernel']}` | {m['dispatches']} | {100 * m['mfma_busy']:.1f} % |\n")
         return
     stats, traffic, ff, fw = summarize(a.kt_dir, a.fetch_dir, a.write_dir, a.timed_steps)
+    steps = workload_steps(stats)
     out = sys.stdout
     if a.commit:
         out.write(f"Traced at commit {a.commit}.\n\n")
+    t = steps.get(TIMED)
+    if t and "timed_step_ns" in t:
+        out.write(f"bench.py's timed region: the last {a.timed_steps} dispatches of each of "
+                  f"{', '.join(f'`{k}`' for k in t['launches'])} (after the untimed clock ramp and warm-up) "
+                  f"average {t['timed_step_ns'] / 1e3:.2f} us per step together = "
+                  f"{t['flops'] / t['timed_step_ns'] / 1e3:.1f} TFLOP/s.\n\n")
+    out.write("## Benchmark workloads (kernel time per step: the averages of the step's launches, summed)\n\n")
+    out.write("| workload | launches per step | us per step | achieved |\n|---|---|---|---|\n")
+    for label, w in steps.items():
+        ach = (f"{w['flops'] / w['step_ns'] / 1e3:.1f} TFLOP/s" if w["flops"]
+               else f"{w['algorithmic_bytes'] / w['step_ns']:.0f} GB/s")
+        out.write(f"| {label} | {' + '.join(f'`{k}`' for k in w['launches'])} | {w['step_ns'] / 1e3:.2f} | {ach} |\n")
+    out.write("\n## Kernel durations (rocprofv3 --kernel-trace, per dispatch, grouped by grid)\n\n")
+    out.write("| kernel | grid (work-items) | benchmark workload | calls | avg us | median us | min us | max us |\n"
+              "|---|---|---|---|---|---|---|---|\n")
     for r in stats:
-        if "timed_avg_ns" in r:
-            flops = BENCH[(r["kernel"], r["grid"])][2]
-            out.write(f"bench.py's timed region: the last {a.timed_steps} `{r['kernel']}` dispatches (after the "
-                      f"untimed clock ramp and warm-up) average {r['timed_avg_ns'] / 1e3:.2f} us = "
-                      f"{flops / r['timed_avg_ns'] / 1e3:.1f} TFLOP/s.\n\n")
-    out.write("## Kernel durations (rocprofv3 --kernel-trace, per dispatch, grouped by grid)\n\n")
-    out.write("| kernel | grid (work-items) | benchmark workload | calls | avg us | median us | min us | max us | "
-              "achieved |\n|---|---|---|---|---|---|---|---|---|\n")
-    for r in stats:
-        bench = BENCH.get((r["kernel"], r["grid"]))
-        ach = ""
-        if bench:
-            _, nbytes, flops = bench
-            ach = (f"{flops / r['avg_ns'] / 1e3:.1f} TFLOP/s" if flops else f"{nbytes / r['avg_ns']:.0f} GB/s")
         out.write(f"| `{r['kernel']}` | {r['grid']} | {r['workload']} | {r['calls']} | {r['avg_ns'] / 1e3:.2f} | "
-                  f"{r['median_ns'] / 1e3:.2f} | {r['min_ns'] / 1e3:.2f} | {r['max_ns'] / 1e3:.2f} | {ach} |\n")
-    out.write(f"\n## HBM traffic per launch (FETCH_SIZE x {ff:.3f}, WRITE_SIZE x {fw:.3f})\n\n")
+                  f"{r['median_ns'] / 1e3:.2f} | {r['min_ns'] / 1e3:.2f} | {r['max_ns'] / 1e3:.2f} |\n")
+    out.write(f"\n## HBM traffic per step (FETCH_SIZE x {ff:.3f}, WRITE_SIZE x {fw:.3f})\n\n")
     out.write("Scale factors: the calibration add reads 512 MiB and writes 256 MiB; the counters read "
               f"{CAL_READ / ff / 2 ** 20:.1f} MiB and {CAL_WRITE / fw / 2 ** 20:.1f} MiB for it.\n\n")
     out.write("| workload | kernel | fetch MB | write MB | traffic MB | algorithmic MB | traffic / algorithmic |\n")

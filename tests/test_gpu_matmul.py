@@ -242,6 +242,43 @@ def test_every_layout_gives_the_same_bits(M, N, K, family):
         np.testing.assert_array_equal(out[name], out[LAYOUTS[0]], err_msg=name)
 
 
+@pytest.mark.parametrize("b_transposed", [False, True])
+def test_last_partial_generation_is_a_second_launch(b_transposed):
+    """4096 x 4096 C (1024 tiles of 128 x 128) on 256 CUs: the first 768 tiles, three per CU,
+    take the multi-workgroup kernel and the last 256 a second launch of the one-generation
+    kernel. Each row tile of C depends on its rows of A alone, so the two launches' C equals,
+    bit for bit, C computed from A's first 3072 rows (768 tiles, one launch) stacked on C from
+    its last 1024 (256 tiles, the one-generation kernel)."""
+    M = N = 4096
+    K = 128
+    g = torch.Generator(device="cuda").manual_seed(21)
+    A = torch.rand((M, K), device="cuda", generator=g) * 2 - 1
+    Bs = torch.rand((N, K) if b_transposed else (K, N), device="cuda", generator=g) * 2 - 1
+    s_bk, s_bn = (1, K) if b_transposed else (N, 1)
+
+    def mm(a):
+        c = torch.full((a.shape[0], N), -1.0, device="cuda")
+        rt.matmul(a, Bs, c, a.shape[0], N, K, K, 1, s_bk, s_bn, N, 1, 8)
+        launches = [(l["kernel"], l["grid"][0]) for l in rt.last_launches()]
+        torch.cuda.synchronize()
+        return c, launches
+
+    c, launches = mm(A)
+    top, l_top = mm(A[:3072])
+    bottom, l_bottom = mm(A[3072:])
+    if rt.device_info()["cu_count"] == 256:
+        assert [k.split("<")[1].split(",")[0] for k, _ in launches] == ["false", "true"], launches
+        assert [grid for _, grid in launches] == [768, 256], launches
+        assert len(l_top) == 1 and len(l_bottom) == 1, (l_top, l_bottom)
+    assert torch.equal(c, torch.cat([top, bottom]))
+    rows = np.random.default_rng(2).choice(M, 48, replace=False)
+    a_np = A.cpu().numpy()[rows]
+    b_np = (Bs.t() if b_transposed else Bs).cpu().numpy()
+    ref = fp64.matmul(a_np, b_np)
+    bound = (K + 2) * 2.0 ** -24 * (np.abs(a_np).astype(np.float64) @ np.abs(b_np).astype(np.float64))
+    assert not (np.abs(c.cpu().numpy()[rows] - ref) > bound).any()
+
+
 def _nan_padded(x, transposed, pad):
     """x (rows x cols) on the GPU in storage whose padding holds NaN: row-major with rows of
     cols + pad floats, or stored transposed with columns of rows + pad floats."""

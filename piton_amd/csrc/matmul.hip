@@ -335,15 +335,22 @@ void gemm_f32_kernel(GemmArgs g) {
 // CU) measured the same; 32 is the default
 constexpr int DKT = PITON_GEMM_DIRECT_KT;
 constexpr int DKH = DKT / 2;               // k per lane half per tile
+#ifndef PITON_GEMM_ONE_GEN_WAVES
+#define PITON_GEMM_ONE_GEN_WAVES 2
+#endif
 #ifndef PITON_GEMM_DIRECT_MB
 #define PITON_GEMM_DIRECT_MB 2
 #endif
 #ifndef PITON_GEMM_DIRECT_NB
 #define PITON_GEMM_DIRECT_NB 2
 #endif
-// 32 x 32 blocks per wave: 2 x 2 at three waves per SIMD measured fastest (4096^3: 140.5
-// TFLOP/s; 4 x 2 and 2 x 4 at 292-296 VGPRs, one wave per SIMD: 137 and 134)
-constexpr int DMB = PITON_GEMM_DIRECT_MB, DNB = PITON_GEMM_DIRECT_NB;
+// 32 x 32 blocks per wave: DMB x DNB (2 x 2: a 128 x 128 workgroup tile), or DMB x DNB_WIDE in
+// the wide form (2 x 4: 128 x 256, one wave per SIMD with its accumulators in AGPRs). Measured
+// with one launch per generation, 4096^3: 2 x 2 0.93 of peak, 2 x 4 0.946, 4 x 2 0.90.
+#ifndef PITON_GEMM_WIDE
+#define PITON_GEMM_WIDE 1
+#endif
+constexpr int DMB = PITON_GEMM_DIRECT_MB, DNB = PITON_GEMM_DIRECT_NB, DNB_WIDE = 2 * DNB;
 constexpr int DBM = 64 * DMB, DBN = 64 * DNB;                           // workgroup tile (2 x 2 waves)
 // ONE_GEN: the launch has at most one workgroup per CU (a wave alone on its SIMD): the next
 // tile's loads are interleaved with this tile's products, one after each MFMA, as in the split
@@ -353,17 +360,21 @@ constexpr int DBM = 64 * DMB, DBN = 64 * DNB;                           // workg
 // is read as float4 chunks along k (lane half h holds k = 16 h + s for s = 0..15); an M- or
 // N-contiguous one one element per k, coalesced across the lanes' 32 consecutive rows or
 // columns. Either way lane (h, l31) supplies the same k at step s, so every layout runs the same
-// MFMA sequence and gives the same bits.
-template <bool ONE_GEN, bool AKC, bool BKC>
-__global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(ONE_GEN ? 2 : PITON_GEMM_DIRECT_WAVES)))
+// MFMA sequence and gives the same bits. NBW: 32 x 32 blocks per wave along N (DNB, or DNB_WIDE
+// in one-generation launches); each output element's k order does not depend on it either.
+template <bool ONE_GEN, bool AKC, bool BKC, int NBW>
+__global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(
+    ONE_GEN ? (NBW > DNB ? 1 : PITON_GEMM_ONE_GEN_WAVES) : PITON_GEMM_DIRECT_WAVES)))
 void gemm_direct_kernel(GemmArgs g) {
+    static_assert(ONE_GEN || NBW == DNB, "the wide form runs one workgroup per CU");
+    constexpr int WNB = NBW, WBN = 64 * NBW;  // blocks per wave along N, workgroup tile columns
     const int t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, l31 = lane & 31;
 
     const int num_pid_m = (int)(g.M / DBM);
-    const int num_pid_n = (int)(g.N / DBN);
+    const int num_pid_n = (int)(g.N / WBN);
     const int pid = g.tile0 + xcd_logical_id(blockIdx.x, gridDim.x, kXcdCount);
     const int in_group = g.group_m * num_pid_n;
     const int group_id = pid / in_group;
@@ -371,7 +382,7 @@ void gemm_direct_kernel(GemmArgs g) {
     const int gsize = min(num_pid_m - first_m, g.group_m);
     const int pid_m = first_m + (pid % in_group) % gsize;
     const int pid_n = (pid % in_group) / gsize;
-    const int64_t m0 = (int64_t)pid_m * DBM, n0 = (int64_t)pid_n * DBN;
+    const int64_t m0 = (int64_t)pid_m * DBM, n0 = (int64_t)pid_n * WBN;
 
     // descriptors bounded at each matrix's last element (whole tiles: every load is inside)
     const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.a), (short)0,
@@ -382,19 +393,19 @@ void gemm_direct_kernel(GemmArgs g) {
     const int64_t s_am = AKC ? g.s_am : 1, s_ak = AKC ? 1 : g.s_ak;
     const int64_t s_bk = BKC ? 1 : g.s_bk, s_bn = BKC ? g.s_bn : 1;
     // per-lane byte offsets of the block's row (A) or column (B) at the lane half's first k
-    uint32_t va[DMB], vb[DNB];
+    uint32_t va[DMB], vb[WNB];
 #pragma unroll
     for (int i = 0; i < DMB; i++)
         va[i] = (uint32_t)(((m0 + wm * 32 * DMB + i * 32 + l31) * s_am + (int64_t)(DKH * half) * s_ak) * 4);
 #pragma unroll
-    for (int i = 0; i < DNB; i++)
-        vb[i] = (uint32_t)(((int64_t)(DKH * half) * s_bk + (n0 + wn * 32 * DNB + i * 32 + l31) * s_bn) * 4);
+    for (int i = 0; i < WNB; i++)
+        vb[i] = (uint32_t)(((int64_t)(DKH * half) * s_bk + (n0 + wn * 32 * WNB + i * 32 + l31) * s_bn) * 4);
     const uint32_t sak4 = (uint32_t)(s_ak * 4), sbk4 = (uint32_t)(s_bk * 4);
 
     constexpr int AQ = AKC ? DKH / 4 : DKH, BQ = BKC ? DKH / 4 : DKH;  // loads per block and K tile
     struct Ops {
         std::conditional_t<AKC, f32x4, float> a[DMB][AQ];
-        std::conditional_t<BKC, f32x4, float> b[DNB][BQ];
+        std::conditional_t<BKC, f32x4, float> b[WNB][BQ];
     };
     auto load = [&](int kt, Ops &o) {
         const int ka = (int)((uint32_t)kt * DKT * sak4), kb = (int)((uint32_t)kt * DKT * sbk4);
@@ -410,7 +421,7 @@ void gemm_direct_kernel(GemmArgs g) {
 #pragma unroll
         for (int q = 0; q < BQ; q++)
 #pragma unroll
-            for (int i = 0; i < DNB; i++) {
+            for (int i = 0; i < WNB; i++) {
                 if constexpr (BKC)
                     o.b[i][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(vb[i] + 16 * q), kb, 0));
                 else
@@ -425,11 +436,11 @@ void gemm_direct_kernel(GemmArgs g) {
         if constexpr (BKC) return o.b[j][s >> 2][s & 3];
         else return o.b[j][s];
     };
-    f32x16 acc[DMB][DNB];
+    f32x16 acc[DMB][WNB];
 #pragma unroll
     for (int i = 0; i < DMB; i++)
 #pragma unroll
-        for (int j = 0; j < DNB; j++)
+        for (int j = 0; j < WNB; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
     auto mul = [&](const Ops &o) {
@@ -438,7 +449,7 @@ void gemm_direct_kernel(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < DMB; i++)
 #pragma unroll
-                for (int j = 0; j < DNB; j++)
+                for (int j = 0; j < WNB; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(aval(o, i, s), bval(o, j, s), acc[i][j], 0, 0, 0);
     };
     // K % (2 DKT) == 0: the tiles come in pairs. The last pair's prefetch loads the last tile
@@ -446,7 +457,7 @@ void gemm_direct_kernel(GemmArgs g) {
     // also keeps the uniform offsets in `soffset` legal (the descriptor's range check covers the
     // per-lane offset only)
     const int nk = (int)(g.K / DKT);
-    constexpr int DLOADS = DMB * AQ + DNB * BQ, DMFMAS = DKH * DMB * DNB;
+    constexpr int DLOADS = DMB * AQ + WNB * BQ, DMFMAS = DKH * DMB * WNB;
     auto interleave = [&]() {
         if constexpr (ONE_GEN) {
 #pragma unroll
@@ -472,8 +483,8 @@ void gemm_direct_kernel(GemmArgs g) {
 #pragma unroll
     for (int mb = 0; mb < DMB; mb++)
 #pragma unroll
-        for (int nb = 0; nb < DNB; nb++) {
-            const int64_t col = n0 + wn * 32 * DNB + nb * 32 + l31;
+        for (int nb = 0; nb < WNB; nb++) {
+            const int64_t col = n0 + wn * 32 * WNB + nb * 32 + l31;
             const float bias = g.bias ? g.bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
@@ -515,8 +526,10 @@ void gemm_direct_kernel(GemmArgs g) {
 #define PITON_SPLIT_WAVES_PER_CU 8
 #endif
 // the direct kernel takes whole-tile shapes with at least this many 128 x 128 tiles per CU
-#ifndef PITON_GEMM_TAIL_LAUNCH
-#define PITON_GEMM_TAIL_LAUNCH 1
+// grids with more tiles than CUs run as one launch per generation of one tile per CU (0: one
+// launch of the multi-workgroup kernel, PITON_GEMM_DIRECT_WAVES workgroups per CU)
+#ifndef PITON_GEMM_GEN_LAUNCHES
+#define PITON_GEMM_GEN_LAUNCHES 1
 #endif
 #ifndef PITON_DIRECT_TILES_PER_CU
 #define PITON_DIRECT_TILES_PER_CU 1
@@ -1018,19 +1031,26 @@ static void launch_b(int bl, const GemmArgs &g, int nwg, hipStream_t st) {
     else PITON_LAUNCH((gemm_f32_kernel<A_L, SCALAR, false>), dim3(nwg), dim3(GTHREADS), 0, st, g);
 }
 
-// one_gen: no more tiles than CUs; akc / bkc: A / B contiguous along K
-static void launch_direct(bool one_gen, bool akc, bool bkc, const GemmArgs &g, unsigned tiles, hipStream_t st) {
+// one_gen: no more tiles than CUs; akc / bkc: A / B contiguous along K; wide: 128 x 256 tiles
+// (one-generation launches only)
+static void launch_direct(bool one_gen, bool wide, bool akc, bool bkc, const GemmArgs &g, unsigned tiles,
+                          hipStream_t st) {
     const dim3 grid(tiles), block(GTHREADS);
-    if (one_gen) {
-        if (akc && !bkc) PITON_LAUNCH((gemm_direct_kernel<true, true, false>), grid, block, 0, st, g);
-        else if (akc) PITON_LAUNCH((gemm_direct_kernel<true, true, true>), grid, block, 0, st, g);
-        else if (!bkc) PITON_LAUNCH((gemm_direct_kernel<true, false, false>), grid, block, 0, st, g);
-        else PITON_LAUNCH((gemm_direct_kernel<true, false, true>), grid, block, 0, st, g);
+    if (wide) {
+        if (akc && !bkc) PITON_LAUNCH((gemm_direct_kernel<true, true, false, DNB_WIDE>), grid, block, 0, st, g);
+        else if (akc) PITON_LAUNCH((gemm_direct_kernel<true, true, true, DNB_WIDE>), grid, block, 0, st, g);
+        else if (!bkc) PITON_LAUNCH((gemm_direct_kernel<true, false, false, DNB_WIDE>), grid, block, 0, st, g);
+        else PITON_LAUNCH((gemm_direct_kernel<true, false, true, DNB_WIDE>), grid, block, 0, st, g);
+    } else if (one_gen) {
+        if (akc && !bkc) PITON_LAUNCH((gemm_direct_kernel<true, true, false, DNB>), grid, block, 0, st, g);
+        else if (akc) PITON_LAUNCH((gemm_direct_kernel<true, true, true, DNB>), grid, block, 0, st, g);
+        else if (!bkc) PITON_LAUNCH((gemm_direct_kernel<true, false, false, DNB>), grid, block, 0, st, g);
+        else PITON_LAUNCH((gemm_direct_kernel<true, false, true, DNB>), grid, block, 0, st, g);
     } else {
-        if (akc && !bkc) PITON_LAUNCH((gemm_direct_kernel<false, true, false>), grid, block, 0, st, g);
-        else if (akc) PITON_LAUNCH((gemm_direct_kernel<false, true, true>), grid, block, 0, st, g);
-        else if (!bkc) PITON_LAUNCH((gemm_direct_kernel<false, false, false>), grid, block, 0, st, g);
-        else PITON_LAUNCH((gemm_direct_kernel<false, false, true>), grid, block, 0, st, g);
+        if (akc && !bkc) PITON_LAUNCH((gemm_direct_kernel<false, true, false, DNB>), grid, block, 0, st, g);
+        else if (akc) PITON_LAUNCH((gemm_direct_kernel<false, true, true, DNB>), grid, block, 0, st, g);
+        else if (!bkc) PITON_LAUNCH((gemm_direct_kernel<false, false, false, DNB>), grid, block, 0, st, g);
+        else PITON_LAUNCH((gemm_direct_kernel<false, false, true, DNB>), grid, block, 0, st, g);
     }
 }
 
@@ -1061,8 +1081,17 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
                         (g.K - 1) * g.s_bk + (g.N - 1) * g.s_bn < (1LL << 29);
     const bool akc = al == VEC_ROW, bkc = bl == VEC_COL;  // the operands contiguous along K
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    // the direct kernel's tiles: 128 x 128, or 128 x 256 when that takes as many generations of
+    // one tile per CU as half as many (each wide tile is twice the work; 3072^3 keeps 128 x 128:
+    // 288 wide tiles would take two generations, the second with 32 tiles, against three of 576)
+    const int64_t ntiles = direct ? (g.M / DBM) * (g.N / DBN) : 0;
+    const int64_t wtiles = direct && g.N % (64 * DNB_WIDE) == 0 ? (g.M / DBM) * (g.N / (64 * DNB_WIDE)) : 0;
+    auto gens = [&](int64_t t) { return (t + cus - 1) / cus; };
+    const bool wide = PITON_GEMM_WIDE && PITON_GEMM_GEN_LAUNCHES && wtiles > 0 && ntiles > cus &&
+                      2 * gens(wtiles) == gens(ntiles);
+    const int64_t dtiles = wide ? wtiles : ntiles;
     const SplitPlan sp =
-        split_ok && !(direct && tiles >= PITON_DIRECT_TILES_PER_CU * cus) ? plan_split(g, cus) : SplitPlan{0, 0, 0};
+        split_ok && !(direct && ntiles >= PITON_DIRECT_TILES_PER_CU * cus) ? plan_split(g, cus) : SplitPlan{0, 0, 0};
     if (sp.nb > 0) {
         // the split kernel's group order runs over its own tile rows
         const int64_t rows = (g.M + 32 * sp.nb - 1) / (32 * sp.nb);
@@ -1071,17 +1100,18 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
         if (sp.nb == 2) launch_split_nb<2>(gs, sp, (unsigned)sp.tiles, st);
         else launch_split_nb<1>(gs, sp, (unsigned)sp.tiles, st);
     } else if (direct) {
-        // the multi-workgroup kernel runs PITON_GEMM_DIRECT_WAVES workgroups per CU at once; a
-        // last generation of at most one tile per CU would run one wave per SIMD with its loads
-        // unhidden, so those tiles go to a second launch of the one-generation kernel
-        const int64_t slots = (int64_t)PITON_GEMM_DIRECT_WAVES * cus, full = tiles / slots * slots;
-        if (PITON_GEMM_TAIL_LAUNCH && tiles > cus && full > 0 && tiles - full > 0 && tiles - full <= cus) {
-            launch_direct(false, akc, bkc, g, (unsigned)full, st);
-            GemmArgs tail = g;
-            tail.tile0 = (int)full;
-            launch_direct(true, akc, bkc, tail, (unsigned)(tiles - full), st);
+        // more tiles than CUs: one launch per generation of (at most) one tile per CU, each on the
+        // one-generation kernel (`tile0` = the launch's first logical tile). One wave per SIMD
+        // with the next tile's loads interleaved into the products keeps the matrix pipe busier
+        // than three workgroups per CU running the plain loop (4096^3: 0.90 -> 0.93 of peak)
+        if (PITON_GEMM_GEN_LAUNCHES && ntiles > cus) {
+            for (int64_t t0 = 0; t0 < dtiles; t0 += cus) {
+                GemmArgs part = g;
+                part.tile0 = (int)t0;
+                launch_direct(true, wide, akc, bkc, part, (unsigned)(dtiles - t0 < cus ? dtiles - t0 : cus), st);
+            }
         } else {
-            launch_direct(tiles <= cus, akc, bkc, g, (unsigned)tiles, st);
+            launch_direct(ntiles <= cus, false, akc, bkc, g, (unsigned)ntiles, st);
         }
     } else if (whole)
         PITON_LAUNCH((gemm_f32_kernel<VEC_ROW, VEC_ROW, true>), dim3(nwg), dim3(GTHREADS), 0, st, g);

@@ -34,16 +34,14 @@ WORKLOADS = {
     "softmax 4096 x 1823": (2 * 4 * 4096 * 1823, None),
     "attention 32 x 1024 x 64 causal": (4 * 32 * 1024 * 64 * 4, 4 * 1024 * 1024 * 64 * 32 // 2),
 }
-# their launches, identified by kernel name and Grid_Size_X (work-items); a step runs each launch
-# of its workload once (the 4096^3 matmul: three 128 x 128 tiles per CU in the first launch,
-# the last 256 tiles in a second)
+# their launches, identified by kernel name and Grid_Size_X (work-items), with the number of
+# times a step runs each (the 4096^3 matmul: two launches of 256 tiles of 128 x 256, one per CU)
 LAUNCHES = {
-    ("gemm_direct_kernel<false, true, false>", 196608): "matmul 4096^3",
-    ("gemm_direct_kernel<true, true, false>", 65536): "matmul 4096^3",
-    ("softmax_rows_kernel<4, true>", 262144): "softmax 4096 x 1024",
-    ("softmax_wg_kernel<2, 512, true>", 2097152): "softmax 4096 x 4096",
-    ("softmax_rows_kernel<8, false>", 196608): "softmax 4096 x 1823",
-    ("attn_fwd_fast<64, true>", 131072): "attention 32 x 1024 x 64 causal",
+    ("gemm_direct_kernel<true, true, false, 4>", 65536): ("matmul 4096^3", 2),
+    ("softmax_rows_kernel<4, true>", 262144): ("softmax 4096 x 1024", 1),
+    ("softmax_wg_kernel<2, 512, true>", 2097152): ("softmax 4096 x 4096", 1),
+    ("softmax_rows_kernel<8, false>", 196608): ("softmax 4096 x 1823", 1),
+    ("attn_fwd_fast<64, true>", 131072): ("attention 32 x 1024 x 64 causal", 1),
 }
 TIMED = "matmul 4096^3"  # the workload of bench.py's timed region
 
@@ -77,27 +75,29 @@ def kernel_stats(kt_dir, timed_steps=0):
         in_order = [d for _, d in sorted(td)]
         d = sorted(in_order)
         row = dict(kernel=k, grid=grid, calls=len(d), avg_ns=sum(d) / len(d), min_ns=d[0],
-                   median_ns=d[len(d) // 2], max_ns=d[-1], workload=LAUNCHES.get((k, grid), ""))
-        if timed_steps and row["workload"] == TIMED and len(in_order) >= timed_steps:
-            last = in_order[-timed_steps:]
+                   median_ns=d[len(d) // 2], max_ns=d[-1], workload=LAUNCHES.get((k, grid), ("", 0))[0],
+                   per_step=LAUNCHES.get((k, grid), ("", 0))[1])
+        if timed_steps and row["workload"] == TIMED and len(in_order) >= timed_steps * row["per_step"]:
+            last = in_order[-timed_steps * row["per_step"]:]
             row["timed_avg_ns"] = sum(last) / len(last)
         rows.append(row)
     return rows
 
 
 def workload_steps(stats):
-    """Per benchmark workload: its launches' average durations summed (the kernel time of one
-    step, gaps between the launches excluded), the timed region's too where known, and the
-    rate that gives."""
+    """Per benchmark workload: its launches' average durations, each times the launches of it a
+    step makes, summed (the kernel time of one step, gaps between the launches excluded), the
+    timed region's too where known."""
     out = {}
     for label, (nbytes, flops) in WORKLOADS.items():
         rows = [r for r in stats if r["workload"] == label]
         if not rows:
             continue
-        step_ns = sum(r["avg_ns"] for r in rows)
-        d = dict(launches=[r["kernel"] for r in rows], step_ns=step_ns, algorithmic_bytes=nbytes, flops=flops)
+        step_ns = sum(r["avg_ns"] * r["per_step"] for r in rows)
+        d = dict(launches=[f"{r['kernel']}" + (f" x {r['per_step']}" if r["per_step"] > 1 else "") for r in rows],
+                 step_ns=step_ns, algorithmic_bytes=nbytes, flops=flops)
         if all("timed_avg_ns" in r for r in rows):
-            d["timed_step_ns"] = sum(r["timed_avg_ns"] for r in rows)
+            d["timed_step_ns"] = sum(r["timed_avg_ns"] * r["per_step"] for r in rows)
         out[label] = d
     return out
 
@@ -124,11 +124,11 @@ def summarize(kt_dir, fetch_dir, write_dir, timed_steps=0):
     f_write = CAL_WRITE / write[cal[0]]
     traffic = {}
     for label, (algo, _) in WORKLOADS.items():
-        keys = [k for k, w in LAUNCHES.items() if w == label and k in fetch and k in write]
+        keys = [k for k, (w, _) in LAUNCHES.items() if w == label and k in fetch and k in write]
         if not keys:
             continue
-        fb = sum(fetch[k] for k in keys) * f_fetch
-        wb = sum(write[k] for k in keys) * f_write
+        fb = sum(fetch[k] * LAUNCHES[k][1] for k in keys) * f_fetch
+        wb = sum(write[k] * LAUNCHES[k][1] for k in keys) * f_write
         traffic[label] = dict(kernel=" + ".join(k[0] for k in keys), grid=[k[1] for k in keys], fetch_bytes=fb,
                               write_bytes=wb, traffic_bytes=fb + wb, algorithmic_bytes=algo)
     return kernel_stats(kt_dir, timed_steps), traffic, f_fetch, f_write
@@ -144,13 +144,13 @@ def mfma_busy(pmc_dir, xcds=8, simds=1024):
     per = {}
     for r in csv.DictReader(open(_one(os.path.join(pmc_dir, "*_counter_collection.csv")))):
         key = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
-        if key not in LAUNCHES or not WORKLOADS[LAUNCHES[key]][1]:
+        if key not in LAUNCHES or not WORKLOADS[LAUNCHES[key][0]][1]:
             continue
         per.setdefault((key, r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
     out = {}
     for (key, _), d in per.items():
         if "GRBM_GUI_ACTIVE" in d and "SQ_VALU_MFMA_BUSY_CYCLES" in d:
-            w = out.setdefault(LAUNCHES[key], dict(kernels=[], dispatches=0, busy=0.0, cycles=0.0))
+            w = out.setdefault(LAUNCHES[key][0], dict(kernels=[], dispatches=0, busy=0.0, cycles=0.0))
             if key[0] not in w["kernels"]:
                 w["kernels"].append(key[0])
             w["dispatches"] += 1
@@ -184,9 +184,9 @@ def main(argv=None):
         out.write(f"Traced at commit {a.commit}.\n\n")
     t = steps.get(TIMED)
     if t and "timed_step_ns" in t:
-        out.write(f"bench.py's timed region: the last {a.timed_steps} dispatches of each of "
+        out.write(f"bench.py's timed region: the last {a.timed_steps} steps' dispatches of "
                   f"{', '.join(f'`{k}`' for k in t['launches'])} (after the untimed clock ramp and warm-up) "
-                  f"average {t['timed_step_ns'] / 1e3:.2f} us per step together = "
+                  f"take {t['timed_step_ns'] / 1e3:.2f} us per step together = "
                   f"{t['flops'] / t['timed_step_ns'] / 1e3:.1f} TFLOP/s.\n\n")
     out.write("## Benchmark workloads (kernel time per step: the averages of the step's launches, summed)\n\n")
     out.write("| workload | launches per step | us per step | achieved |\n|---|---|---|---|\n")

@@ -243,12 +243,12 @@ def test_every_layout_gives_the_same_bits(M, N, K, family):
 
 
 @pytest.mark.parametrize("b_transposed", [False, True])
-def test_last_partial_generation_is_a_second_launch(b_transposed):
-    """4096 x 4096 C (1024 tiles of 128 x 128) on 256 CUs: the first 768 tiles, three per CU,
-    take the multi-workgroup kernel and the last 256 a second launch of the one-generation
-    kernel. Each row tile of C depends on its rows of A alone, so the two launches' C equals,
-    bit for bit, C computed from A's first 3072 rows (768 tiles, one launch) stacked on C from
-    its last 1024 (256 tiles, the one-generation kernel)."""
+def test_generations_run_as_separate_launches(b_transposed):
+    """4096 x 4096 C on 256 CUs runs as two launches of 256 tiles of 128 x 256, one per CU each;
+    C from A's first 3072 rows as three launches of 256 tiles of 128 x 128 (384 wide tiles would
+    take two launches, the second half empty); C from its last 1024 rows as one launch of 256
+    tiles of 128 x 128. Each row tile of C depends on its rows of A alone and each element's k
+    order is the same in every form, so C equals the two parts stacked, bit for bit."""
     M = N = 4096
     K = 128
     g = torch.Generator(device="cuda").manual_seed(21)
@@ -267,9 +267,10 @@ def test_last_partial_generation_is_a_second_launch(b_transposed):
     top, l_top = mm(A[:3072])
     bottom, l_bottom = mm(A[3072:])
     if rt.device_info()["cu_count"] == 256:
-        assert [k.split("<")[1].split(",")[0] for k, _ in launches] == ["false", "true"], launches
-        assert [grid for _, grid in launches] == [768, 256], launches
-        assert len(l_top) == 1 and len(l_bottom) == 1, (l_top, l_bottom)
+        assert [grid for _, grid in launches] == [256] * 2, launches
+        assert all(k.startswith("gemm_direct_kernel<true,") and k.endswith("DNB_WIDE>") for k, _ in launches)
+        assert [grid for _, grid in l_top] == [256] * 3 and [grid for _, grid in l_bottom] == [256]
+        assert all(k.endswith(", DNB>") for k, _ in l_top + l_bottom), (l_top, l_bottom)
     assert torch.equal(c, torch.cat([top, bottom]))
     rows = np.random.default_rng(2).choice(M, 48, replace=False)
     a_np = A.cpu().numpy()[rows]

@@ -7,8 +7,7 @@ import pytest
 
 from piton_amd import profiling
 
-GEMM = "void piton::gemm_direct_kernel<false, true, false>(piton::GemmArgs)"  # 768 tiles
-TAIL = "void piton::gemm_direct_kernel<true, true, false>(piton::GemmArgs)"   # the last 256
+GEMM = "void piton::gemm_direct_kernel<true, true, false, 4>(piton::GemmArgs)"  # 256 tiles, two a step
 ADD = "void piton::add_vec4_kernel(float const*, float const*, float*, long)"
 COLS = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value", "Start_Timestamp",
         "End_Timestamp"]
@@ -34,36 +33,36 @@ def write_trace(d, rows):
 
 def test_traffic_is_scaled_by_the_calibration_add(tmp_path):
     kt, fe, wr = (str(tmp_path / n) for n in ("kt", "fetch", "write"))
-    write_trace(kt, [(GEMM, 196608, 0, 1_000_000), (TAIL, 65536, 1_000_000, 1_300_000),
-                     (GEMM, 196608, 2_000_000, 3_100_000), (TAIL, 65536, 3_100_000, 3_400_000)])
+    # two steps of two launches; the second step's launches take 300 us each
+    write_trace(kt, [(GEMM, 65536, 1_000_000 * i, 1_000_000 * i + (200_000 if i < 2 else 300_000))
+                     for i in range(4)])
     # the counters read half the calibration add's true bytes: the factors are 2
     write_pmc(fe, [(1, ADD, 64 * 2 ** 20 // 4, "FETCH_SIZE", profiling.CAL_READ / 2 / 1024, 0, 1),
-                   (2, GEMM, 196608, "FETCH_SIZE", 400_000.0, 0, 1), (3, TAIL, 65536, "FETCH_SIZE", 100_000.0, 1, 2)])
+                   (2, GEMM, 65536, "FETCH_SIZE", 100_000.0, 0, 1), (3, GEMM, 65536, "FETCH_SIZE", 120_000.0, 1, 2)])
     write_pmc(wr, [(1, ADD, 64 * 2 ** 20 // 4, "WRITE_SIZE", profiling.CAL_WRITE / 2 / 1024, 0, 1),
-                   (2, GEMM, 196608, "WRITE_SIZE", 30_000.0, 0, 1), (3, TAIL, 65536, "WRITE_SIZE", 10_000.0, 1, 2)])
+                   (2, GEMM, 65536, "WRITE_SIZE", 10_000.0, 0, 1), (3, GEMM, 65536, "WRITE_SIZE", 10_000.0, 1, 2)])
     stats, traffic, ff, fw = profiling.summarize(kt, fe, wr, timed_steps=1)
     assert ff == pytest.approx(2.0) and fw == pytest.approx(2.0)
-    t = traffic["matmul 4096^3"]  # a step's two launches together
-    assert t["fetch_bytes"] == pytest.approx(2 * 500_000 * 1024)
-    assert t["write_bytes"] == pytest.approx(2 * 40_000 * 1024)
+    t = traffic["matmul 4096^3"]  # per step: two launches of the average dispatch
+    assert t["fetch_bytes"] == pytest.approx(2 * 2 * 110_000 * 1024)
+    assert t["write_bytes"] == pytest.approx(2 * 2 * 10_000 * 1024)
     assert t["algorithmic_bytes"] == 3 * 4096 * 4096 * 4
-    assert stats[0]["kernel"] == "gemm_direct_kernel<false, true, false>"
-    assert stats[0]["calls"] == 2 and stats[0]["avg_ns"] == pytest.approx(1_050_000)
+    assert stats[0]["calls"] == 4 and stats[0]["avg_ns"] == pytest.approx(250_000)
     steps = profiling.workload_steps(stats)["matmul 4096^3"]
-    assert steps["step_ns"] == pytest.approx(1_050_000 + 300_000)
-    assert steps["timed_step_ns"] == pytest.approx(1_100_000 + 300_000)  # the last dispatch of each
+    assert steps["step_ns"] == pytest.approx(2 * 250_000)
+    assert steps["timed_step_ns"] == pytest.approx(2 * 300_000)  # the last step's two dispatches
 
 
 def test_mfma_busy(tmp_path):
     d = str(tmp_path / "pmc")
     # 1 ms at 2.4 GHz on each of 8 XCDs with the 1024 SIMDs' MFMA pipes busy 90 % of it, then
-    # 0.5 ms at 60 %: 80 % over the step
+    # 0.5 ms at 60 %: 80 % over both
     gui, gui2 = 8 * 2.4e6, 8 * 1.2e6
     busy, busy2 = 0.9 * 2.4e6 * 1024, 0.6 * 1.2e6 * 1024
-    write_pmc(d, [(7, GEMM, 196608, "GRBM_GUI_ACTIVE", gui, 5_000, 1_005_000),
-                  (7, GEMM, 196608, "SQ_VALU_MFMA_BUSY_CYCLES", busy, 5_000, 1_005_000),
-                  (8, TAIL, 65536, "GRBM_GUI_ACTIVE", gui2, 1_005_000, 1_505_000),
-                  (8, TAIL, 65536, "SQ_VALU_MFMA_BUSY_CYCLES", busy2, 1_005_000, 1_505_000),
+    write_pmc(d, [(7, GEMM, 65536, "GRBM_GUI_ACTIVE", gui, 5_000, 1_005_000),
+                  (7, GEMM, 65536, "SQ_VALU_MFMA_BUSY_CYCLES", busy, 5_000, 1_005_000),
+                  (8, GEMM, 65536, "GRBM_GUI_ACTIVE", gui2, 1_005_000, 1_505_000),
+                  (8, GEMM, 65536, "SQ_VALU_MFMA_BUSY_CYCLES", busy2, 1_005_000, 1_505_000),
                   (9, ADD, 1024, "GRBM_GUI_ACTIVE", 100.0, 0, 10)])
     m = profiling.mfma_busy(d)
     assert list(m) == ["matmul 4096^3"]

@@ -13,7 +13,8 @@
 //     stores when rows, strides and pointers allow it (LDS row pitch 129), else 64 x 64 scalar
 //     tiles (row stride 65); reads and writes are coalesced rows either way. Measured at
 //     8192 x 8192: 64 x 64 scalar 130 us, 64 x 128 float4 113 us, 128 x 128 float4 with 256 /
-//     512 / 1024 threads 106 / 99 / 98 us (a copy of the same bytes: 81 us).
+//     512 / 1024 threads 106 / 99 / 98 us, and 90 us with the tiles walked down the columns
+//     (a copy of the same bytes: 81 us).
 #include <math.h>
 
 #include "common.h"
@@ -168,11 +169,15 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float *x, float *o
 #endif
 constexpr int kTrR = PITON_TR_R, kTrC = PITON_TR_C, kTrT = PITON_TR_T;
 __global__ __launch_bounds__(kTrT) void transpose_vec_kernel(const float *x, float *out, int64_t n_rows, int64_t n_cols,
-                                                             int64_t stride_x, int64_t stride_out, int64_t tiles_c) {
+                                                             int64_t stride_x, int64_t stride_out, int64_t tiles_r) {
     constexpr int LPR = kTrC / 4, LP = kTrR * kTrC / (4 * kTrT);  // load: threads per input row, passes
     constexpr int SPR = kTrR / 4, SP = LP;                         // store: threads per output row, passes
     __shared__ float tile[kTrR][kTrC + 1];
-    const int64_t r0 = (int64_t)(blockIdx.x / tiles_c) * kTrR, c0 = (int64_t)(blockIdx.x % tiles_c) * kTrC;
+    // consecutive workgroups walk down a column band of tiles: the workgroups in flight write
+    // long runs of the same output rows (8192^2: 0.69 -> 0.74 of HBM; across 8192^2, 4096^2,
+    // 16384 x 4096 and 4096 x 16384 0.63 -> 0.68 on average, where groups of 4-32 row tiles
+    // measured 0.64-0.675 and the XCD-contiguous order 0.63)
+    const int64_t r0 = (int64_t)(blockIdx.x % tiles_r) * kTrR, c0 = (int64_t)(blockIdx.x / tiles_r) * kTrC;
     const int t = threadIdx.x;
     const int cq = t % LPR, rb = t / LPR;
     f32x4 v[LP];
@@ -322,7 +327,7 @@ int32_t piton_mi355x_transpose(const float *x, float *out, int64_t n_rows, int64
     if (vec) {
         const int64_t tr = (n_rows + kTrR - 1) / kTrR, tc = (n_cols + kTrC - 1) / kTrC;
         PITON_LAUNCH(transpose_vec_kernel, dim3((unsigned)(tr * tc)), dim3(kTrT), 0, (hipStream_t)stream, x, out,
-                           n_rows, n_cols, stride_x, stride_out, tc);
+                           n_rows, n_cols, stride_x, stride_out, tr);
     } else {
         PITON_LAUNCH(transpose_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, (hipStream_t)stream,
                            x, out, n_rows, n_cols, stride_x, stride_out, tiles_n);

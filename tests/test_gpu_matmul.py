@@ -280,6 +280,34 @@ def test_generations_run_as_separate_launches(b_transposed):
     assert not (np.abs(c.cpu().numpy()[rows] - ref) > bound).any()
 
 
+@pytest.mark.parametrize("M", [2048, 1024])
+def test_dense_and_linear_epilogues_in_generation_launches(M):
+    """The bias, ReLU and residual epilogue in the register-direct kernel's one-launch-per-
+    generation forms: 2048 x 4096 (512 tiles of 128 x 128, so one launch of 256 wide tiles) and
+    1024 x 4096 (256 tiles, one launch of 128 x 128 tiles). Dyadic inputs: every product and sum
+    is exact, so the result equals numpy's bit for bit."""
+    N, K = 4096, 64
+    rng = np.random.default_rng(M + 5)
+    a, b, bias = dyadic(rng, (M, K)), dyadic(rng, (K, N)), dyadic(rng, (N,))
+    res = dyadic(rng, (M, N))
+    x, w, tb, tr = (torch.from_numpy(v).cuda() for v in (a, b, bias, res))
+    y = torch.full((M, N), -7.0, device="cuda")
+    rt.dense(x, w, tb, y, M, N, K, add_bias=True, relu=True)
+    dense_launches = [(l["kernel"], l["grid"][0]) for l in rt.last_launches()]
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), np.maximum(a @ b + bias, 0))
+    y.fill_(-7.0)
+    rt.linear(x, K, w, tb, tr, N, y, N, M, N, K, relu=False)
+    linear_launches = [(l["kernel"], l["grid"][0]) for l in rt.last_launches()]
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), a @ b + bias + res)
+    if rt.device_info()["cu_count"] == 256:
+        for launches in (dense_launches, linear_launches):
+            assert len(launches) == 1 and launches[0][1] == 256, launches
+            assert launches[0][0].startswith("gemm_direct_kernel<true,"), launches
+            assert launches[0][0].endswith("DNB_WIDE>" if M == 2048 else ", DNB>"), launches
+
+
 def _nan_padded(x, transposed, pad):
     """x (rows x cols) on the GPU in storage whose padding holds NaN: row-major with rows of
     cols + pad floats, or stored transposed with columns of rows + pad floats."""

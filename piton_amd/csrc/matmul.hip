@@ -308,23 +308,24 @@ void gemm_f32_kernel(GemmArgs g) {
         }
 }
 
-// whole-tile row-major shapes take the register-direct kernel below (1) or the LDS kernel (0)
+// whole-tile shapes (row- or column-major operands) take the register-direct kernel below (1)
+// or the LDS kernel (0)
 #ifndef PITON_GEMM_DIRECT
 #define PITON_GEMM_DIRECT 1
 #endif
 
-// Whole-tile row-major shapes without LDS: every wave loads its own MFMA operands from memory
-// straight into registers, so there is no LDS staging and no barrier, and the waves of a
-// workgroup run independently. Within a K tile of 32, lane half h supplies k = 16h + s at MFMA
-// step s (the contraction order inside the tile is free as long as A and B agree), which
-// makes each lane's A operands 16 consecutive floats of its row (four 16-byte loads) and its
-// B operands 16 rows of its column (one 4-byte load per row, 128 contiguous bytes per
-// half-wave). Operands of tile k+1 are loaded while tile k multiplies (two register sets,
-// the loop unrolled by two). Buffer descriptors carry the matrices (each < 2 GiB); every load
-// lies inside them. 146 VGPRs:
-// three workgroups per CU. At 4096^3 this runs ~5 % faster than the LDS kernel, whose two
-// barriers per K tile left the matrix pipe idle 14 % of the time; at four workgroups per CU
-// (128 VGPRs) it spills and runs 10 % slower.
+// Whole-tile shapes without LDS: every wave loads its own MFMA operands from memory straight
+// into registers, so there is no LDS staging and no barrier, and the waves of a workgroup run
+// independently. Within a K tile of 32, lane half h supplies k = 16h + s at MFMA step s (the
+// contraction order inside the tile is free as long as A and B agree), which makes a row-major
+// A's operands 16 consecutive floats of the lane's row (four 16-byte loads) and a row-major B's
+// 16 rows of its column (one 4-byte load per row, 128 contiguous bytes per half-wave).
+// Operands of tile k+1 are loaded while tile k multiplies (two register sets, the loop unrolled
+// by two). Buffer descriptors carry the matrices (each < 2 GiB); every load lies inside them.
+// The plain loop (ONE_GEN false, 146 VGPRs, three workgroups per CU) ran 4096^3 ~5 % faster
+// than the LDS kernel, whose two barriers per K tile left the matrix pipe idle 14 % of the
+// time; grids of more tiles than CUs now run as one launch per generation of one workgroup per
+// CU on the interleaved form (launch_gemm), which is faster again.
 #ifndef PITON_GEMM_DIRECT_KT
 #define PITON_GEMM_DIRECT_KT 32
 #endif

@@ -158,6 +158,26 @@ def test_group_order_does_not_change_bits(group):
     assert torch.equal(base, other)
 
 
+@pytest.mark.parametrize("group", [1, 3, 7, 64, 2 ** 31 - 1])
+def test_group_order_across_generation_launches(group):
+    """4096 x 4096 x 64 runs as two launches of 256 wide tiles whose logical ids continue from
+    one launch to the next (tile0): any GROUP_SIZE_M orders the tiles differently across the
+    launches and gives the same bits, every element written once (C prefilled with NaN)."""
+    g = torch.Generator(device="cuda").manual_seed(13)
+    a = torch.rand((4096, 64), device="cuda", generator=g)
+    b = torch.rand((64, 4096), device="cuda", generator=g)
+
+    def mm(group_m):
+        c = torch.full((4096, 4096), float("nan"), device="cuda")
+        rt.matmul(a, b, c, 4096, 4096, 64, 64, 1, 4096, 1, 4096, 1, group_m)
+        torch.cuda.synchronize()
+        return c
+
+    base, other = mm(8), mm(group)
+    assert not torch.isnan(other).any()
+    assert torch.equal(base, other)
+
+
 @pytest.mark.parametrize("group", [1, 3, 64, 2 ** 31 - 1])
 def test_group_order_does_not_change_bits_whole_tiles(group):
     g = torch.Generator(device="cuda").manual_seed(12)

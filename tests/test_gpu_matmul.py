@@ -194,6 +194,33 @@ def _sweep_shape(rng, kind):
     return tuple(int(rng.integers(1, 400)) for _ in range(3))  # ragged edges
 
 
+def test_seeded_large_whole_tile_sweep():
+    """16 seeded whole-tile shapes past one generation of tiles (the register-direct kernel in
+    one launch per generation, 128 x 128 or 128 x 256 tiles), each operand row- or column-major
+    with padded strides, random GROUP_SIZE_M: 48 sampled rows of every C within the float32
+    bound of the float64 product, and C's padding columns untouched."""
+    rng = np.random.default_rng(2027)
+    for case in range(16):
+        M, N = (int(rng.integers(8, 33)) * 128 for _ in range(2))
+        K = int(rng.integers(1, 9)) * 64
+        a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+        b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        lay = int(rng.integers(0, 4))
+        pad = int(rng.integers(0, 3)) * 4
+        A, B = _nan_padded(a, lay & 1, pad), _nan_padded(b, lay & 2, pad)
+        C = torch.full((M, N + 4), -7.0, device="cuda")
+        group = int(rng.choice([1, 3, 8, 2 ** 31 - 1]))
+        rt.matmul(A, B, C, M, N, K, A.stride(0), A.stride(1), B.stride(0), B.stride(1), N + 4, 1, group)
+        kernel = rt.last_launches()[0]["kernel"]
+        torch.cuda.synchronize()
+        rows = rng.choice(M, 48, replace=False)
+        got = C[torch.from_numpy(rows).cuda()].cpu().numpy()
+        ref = fp64.matmul(a[rows], b)
+        bound = (K + 2) * 2.0 ** -24 * (np.abs(a[rows]).astype(np.float64) @ np.abs(b).astype(np.float64))
+        assert not (np.abs(got[:, :N] - ref) > bound).any(), (case, M, N, K, lay, pad, group, kernel)
+        assert (got[:, N:] == -7.0).all(), (case, kernel)
+
+
 def test_seeded_shape_sweep_against_float64():
     """48 seeded shapes and layouts in one process (whole tiles for the register-direct and the
     LDS kernels, ragged edges, padded rows, A or B stored transposed); every element within the

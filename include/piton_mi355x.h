@@ -192,6 +192,20 @@ PITON_API int32_t piton_mi355x_attn_decode(const float *q, const float *k, const
                                  int64_t stride_oh, int64_t n_keys, int64_t batch, int64_t n_heads,
                                  int32_t head_dim, void *stream);
 
+/* A decode step of one decoder layer in one launch: for each sequence b < batch, the new row
+ * LN(x[b]) W + bias (LN as in piton_mi355x_linear_ln, W [d_model, 3 d_model] row-major, bias
+ * nullable) is written to cache row (n_keys - 1) * batch + b (q | k | v, each d_model wide, row
+ * stride ldc), and out[b, h*64 .. h*64+63] gets head h's attention of that q over the keys
+ * 0 .. n_keys-1 of the position-major cache (row t * batch + b: k at column d_model + h*64, v at
+ * 2 d_model + h*64). Equal to piton_mi355x_linear_ln followed by piton_mi355x_attn_decode to
+ * rounding. Needs head_dim 64, d_model = n_heads * 64 a multiple of 256 up to 1024, n_keys <= 256,
+ * W and the cache 16-byte aligned with ldc % 4 == 0; otherwise PITON_EUNSUPPORTED. No reference
+ * counterpart (the reference has no decoder): it serves the decoder's per-token steps. */
+PITON_API int32_t piton_mi355x_decode_layer(const float *x, int64_t ldx, float eps, const float *w,
+                                            const float *bias, float *cache, int64_t ldc, float *out,
+                                            int64_t ldo, float sm_scale, int64_t n_keys, int64_t batch,
+                                            int64_t n_heads, int32_t head_dim, int64_t d_model, void *stream);
+
 /* ---- the perf suite's primitives (perf/suite.py:323-351): elementwise over n elements ---- */
 
 /* out = x. Replaces copy_kernel (examples/primitive_kernels.py:12-17). */

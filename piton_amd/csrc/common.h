@@ -93,7 +93,8 @@ static inline PhaseRecord *phase_slot() { return nullptr; }
 #define PITON_PHASE_TU(name)
 #endif
 // kernel ids of the trace records
-constexpr uint32_t kPhaseSoftmaxRows = 1, kPhaseSoftmaxWg = 2, kPhaseAttnFast = 3, kPhaseAttnDecodeShort = 4;
+constexpr uint32_t kPhaseSoftmaxRows = 1, kPhaseSoftmaxWg = 2, kPhaseAttnFast = 3, kPhaseAttnDecodeShort = 4,
+                   kPhaseDecodeLayer = 5;
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }

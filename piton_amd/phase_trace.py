@@ -1,5 +1,5 @@
-"""Launch phases of the HBM-bound softmax, the one-generation attention kernel and the decode
-attention of the KV-cached decoder (diagnostics).
+"""Launch phases of the HBM-bound softmax, the one-generation attention kernel, the decode
+attention of the KV-cached decoder and its fused decode step (diagnostics).
 
 `python -m piton_amd.phase_trace` builds a traced copy of the library beside the product one
 (-DPITON_PHASE_TRACE: every traced wave keeps s_memrealtime stamps -- a 100 MHz clock shared by
@@ -66,7 +66,8 @@ def _trace(tu: str, fn, launches: int):
     graph.replay()
     torch.cuda.synchronize()
     t = np.frombuffer(log.cpu().numpy().tobytes(), dtype=np.uint64).reshape(launches, K_PHASE_WAVES, rec // 8)
-    return [[tuple(int(x) for x in r[:4]) for r in t[k][t[k][:, 0] > 0]] for k in range(launches)]
+    # (t0, t1, t2, t3, kernel | wave << 32) per traced wave
+    return [[tuple(int(x) for x in r[:5]) for r in t[k][t[k][:, 0] > 0]] for k in range(launches)]
 
 
 def _summary(launches, stamps: int, nbytes: int | None = None):
@@ -137,6 +138,37 @@ def decode_phases(n_keys: int, batch: int = 64, heads: int = 4, d_head: int = 64
     return _summary(per, 4)
 
 
+def decode_layer_phases(n_keys: int, batch: int = 64, heads: int = 4, d_head: int = 64, launches: int = 12):
+    """TinyGPT's fused decode step of a layer (piton_mi355x_decode_layer): per launch, medians
+    over waves of the layernorm phase (to the barrier after it), of the projection on waves 0-2
+    and of the cache copies on wave 3 (both from that barrier), and of the attention after the
+    two meet."""
+    import torch
+
+    from .runtime import mi355x as rt
+    D = heads * d_head
+    g = torch.Generator(device="cuda").manual_seed(n_keys)
+    cache = torch.randn((n_keys * batch, 3 * D), device="cuda", generator=g)
+    x = torch.randn((batch, D), device="cuda", generator=g)
+    w = torch.randn((D, 3 * D), device="cuda", generator=g) * 0.05
+    att = torch.empty((batch, D), device="cuda")
+    per = _trace("decode_layer", lambda i: rt.decode_layer(x, D, 1e-5, w, None, cache, 3 * D, att, D, d_head ** -0.5,
+                                                          n_keys, batch, heads, d_head, D), launches)
+    rows = []
+    for k in range(1, len(per) - 1):
+        ls = per[k]
+        t0 = min(r[0] for r in ls)
+        proj = [r for r in ls if (r[4] >> 32) % 4 != 3]
+        copy = [r for r in ls if (r[4] >> 32) % 4 == 3]
+        rows.append(dict(layernorm=statistics.median(r[1] - r[0] for r in ls),
+                         projection=statistics.median(r[2] - r[1] for r in proj),
+                         cache_copies=statistics.median(r[2] - r[1] for r in copy),
+                         attention=statistics.median(r[3] - r[2] for r in ls),
+                         end=max(r[3] for r in ls) - t0,
+                         gap_to_next=min(r[0] for r in per[k + 1]) - max(r[3] for r in ls)))
+    return {key: statistics.median(r[key] for r in rows) * TICK_US for key in rows[0]}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--no-build", action="store_true", help="use the traced library already built")
@@ -164,6 +196,14 @@ def main():
         print(f"| decode attention 64 x 4 heads x 64, {nk} keys | {int(m['waves'])} | {us(m['last_wave_start'])} | "
               f"{us(m['first_data'])} (K, V in) | {us(m['wave_wait'])} | {us(m['end'])} | {us(m['gap_to_next'])} | "
               f"per wave: scores and max {us(m['loop'])}, exp, sum, P V {us(m['merge'])} |")
+    print()
+    print("| fused decode step, 64 x 4 heads x 64 | layernorm | projection (waves 0-2) | cache copies (wave 3) | "
+          "attention | last wave ends | gap to next launch |")
+    print("|---|---|---|---|---|---|---|")
+    for nk in (96, 160):
+        m = decode_layer_phases(nk)
+        print(f"| {nk} keys | {us(m['layernorm'])} | {us(m['projection'])} | {us(m['cache_copies'])} | "
+              f"{us(m['attention'])} | {us(m['end'])} | {us(m['gap_to_next'])} |")
 
 
 if __name__ == "__main__":

@@ -74,8 +74,13 @@ def seeded_prompts(batch: int = 64, length: int = 32, vocab: int = 256, seed: in
 class TinyGPT:
     """Device-resident weights and buffers for `batch` sequences of up to cfg.context tokens."""
 
-    def __init__(self, weights: dict, cfg: Config = Config(), batch: int = 64, device="cuda"):
+    def __init__(self, weights: dict, cfg: Config = Config(), batch: int = 64, device="cuda",
+                 fused_decode: bool = True):
+        """fused_decode: decode steps run each layer's layernorm, QKV projection and attention
+        as one piton_mi355x_decode_layer launch where the shapes allow (head_dim 64), instead
+        of linear_ln + attn_decode."""
         self.cfg, self.B = cfg, batch
+        self.fused_decode = fused_decode
         self.w = {k: torch.as_tensor(np.ascontiguousarray(v)).to(device) for k, v in weights.items()}
         D, F, V, C = cfg.d_model, cfg.d_mlp, cfg.vocab, cfg.context
         rows = C * batch
@@ -108,11 +113,15 @@ class TinyGPT:
             w = lambda k: self.w[f"{k}{i}"]  # noqa: E731
             cache = self.qkv[i]
             qkv = cache[r0:r0 + n]
-            if fuse_ln:
-                rt.linear_ln(x, D, cfg.eps, w("wqkv"), w("bqkv"), None, 0, qkv, 3 * D, n, 3 * D, D)
+            if p0 > 0 and self.fused_decode and Dh == 64 and D % 256 == 0 and p1 <= 256:
+                # a decode step: layernorm, QKV into the cache row and attention in one launch
+                rt.decode_layer(x, D, cfg.eps, w("wqkv"), w("bqkv"), cache, 3 * D, att, D, scale, p1, B, H, Dh, D)
             else:
-                rt.layernorm(x, h, D, cfg.eps, n, D)
-                rt.linear(h, D, w("wqkv"), w("bqkv"), None, 0, qkv, 3 * D, n, 3 * D, D)
+                if fuse_ln:
+                    rt.linear_ln(x, D, cfg.eps, w("wqkv"), w("bqkv"), None, 0, qkv, 3 * D, n, 3 * D, D)
+                else:
+                    rt.layernorm(x, h, D, cfg.eps, n, D)
+                    rt.linear(h, D, w("wqkv"), w("bqkv"), None, 0, qkv, 3 * D, n, 3 * D, D)
             if p0 == 0:
                 # prefix: batched causal flash attention over positions [0, p1)
                 rt.attn_fwd_batched(cache, cache[:, D:], cache[:, 2 * D:], self.att, scale,
@@ -121,8 +130,9 @@ class TinyGPT:
             else:
                 if p1 != p0 + 1:
                     raise ValueError("decode steps take one position at a time")
-                rt.attn_decode(qkv, cache[:, D:], cache[:, 2 * D:], att, scale, 3 * D, Dh, 3 * D, Dh,
-                               B * 3 * D, 3 * D, Dh, B * 3 * D, D, Dh, p1, B, H, Dh)
+                if not (self.fused_decode and Dh == 64 and D % 256 == 0 and p1 <= 256):
+                    rt.attn_decode(qkv, cache[:, D:], cache[:, 2 * D:], att, scale, 3 * D, Dh, 3 * D, Dh,
+                                   B * 3 * D, 3 * D, Dh, B * 3 * D, D, Dh, p1, B, H, Dh)
             rt.linear(att, D, w("wo"), w("bo"), x, D, x, D, n, D, D)
             if fuse_ln:
                 rt.linear_ln(x, D, cfg.eps, w("w1"), w("b1"), None, 0, mlp, F, n, F, D, relu=True)

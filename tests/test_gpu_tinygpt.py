@@ -197,6 +197,103 @@ def test_short_and_long_decode_kernels_agree(dh):
     np.testing.assert_array_equal(short.view(np.uint32), long_.view(np.uint32))
 
 
+def _decode_layer_case(B, H, n_keys, pad, seed):
+    """Random decode-step inputs in the decoder's layout: x [B, Dm] rows (stride Dm + 4 pad),
+    W [Dm, 3 Dm], bias, a position-major cache of n_keys + 2 positions (row t*B + b, stride
+    3 Dm + 4 pad) whose rows from position n_keys - 1 on are NaN."""
+    rng = np.random.default_rng(seed)
+    Dm = 64 * H
+    x = (rng.standard_normal((B, Dm + 4 * pad)) * 2 + 0.5).astype(np.float32)
+    w = (rng.standard_normal((Dm, 3 * Dm)) * 0.06).astype(np.float32)
+    b = (rng.standard_normal(3 * Dm) * 0.1).astype(np.float32)
+    ldc = 3 * Dm + 4 * pad
+    cache = rng.standard_normal(((n_keys + 2) * B, ldc)).astype(np.float32)
+    cache[(n_keys - 1) * B:] = np.nan
+    return x, w, b, cache, Dm, ldc
+
+
+def _decode_layer_ref(x, w, b, cache, B, H, n_keys, Dm):
+    """float64: the new rows LN(x) W + b, and each head's attention over the cached keys and the
+    new one (scale 1/8)."""
+    y = tinygpt64.layernorm(x[:, :Dm].astype(np.float64), 1e-5) @ w + b
+    kv = cache[:(n_keys - 1) * B, :3 * Dm].astype(np.float64).reshape(n_keys - 1, B, 3 * Dm)
+    kv = np.concatenate([kv, y[None]], axis=0)  # [n_keys, B, 3 Dm]
+    att = np.empty((B, Dm))
+    for h in range(H):
+        q = y[:, h * 64:(h + 1) * 64]
+        k = kv[:, :, Dm + h * 64:Dm + (h + 1) * 64]
+        v = kv[:, :, 2 * Dm + h * 64:2 * Dm + (h + 1) * 64]
+        s = np.einsum("bd,tbd->bt", q, k) / 8
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        att[:, h * 64:(h + 1) * 64] = np.einsum("bt,tbd->bd", p, v)
+    return y, att
+
+
+@pytest.mark.parametrize("B,H,n_keys,pad", [(64, 4, 1, 0), (64, 4, 2, 0), (64, 4, 97, 0), (64, 4, 160, 1),
+                                            (64, 4, 256, 0), (3, 8, 130, 3), (5, 16, 33, 0)])
+def test_decode_layer_matches_float64_and_the_two_launches(B, H, n_keys, pad):
+    """The fused decode step (layernorm, QKV projection into the cache row, attention) against
+    float64 and against linear_ln + attn_decode: the new cache row and the attention output
+    within float32 tolerance, every other cache row untouched (the NaN rows past the new one are
+    never read), padding columns untouched."""
+    x, w, b, cache, Dm, ldc = _decode_layer_case(B, H, n_keys, pad, seed=n_keys * 31 + H)
+    y_ref, att_ref = _decode_layer_ref(x, w, b, cache, B, H, n_keys, Dm)
+    tx, tw, tb = (torch.from_numpy(t).cuda() for t in (x, w, b))
+    tc = torch.from_numpy(cache).cuda()
+    ldo = Dm + 2 * pad
+    out = torch.full((B, ldo), -5.0, device="cuda")
+    rt.decode_layer(tx, Dm + 4 * pad, 1e-5, tw, tb, tc, ldc, out, ldo, 1 / 8, n_keys, B, H, 64, Dm)
+    torch.cuda.synchronize()
+    got_c, got = tc.cpu().numpy(), out.cpu().numpy()
+    new = slice((n_keys - 1) * B, n_keys * B)
+    assert fp64.rel_fro(got_c[new, :3 * Dm], y_ref) <= 2e-6
+    assert fp64.rel_fro(got[:, :Dm], att_ref) <= 1e-5
+    assert (got[:, Dm:] == -5.0).all()
+    before = np.ones(len(cache), bool)
+    before[new] = False
+    np.testing.assert_array_equal(got_c[before].view(np.uint32), cache[before].view(np.uint32))
+    np.testing.assert_array_equal(got_c[new, 3 * Dm:].view(np.uint32), cache[new, 3 * Dm:].view(np.uint32))
+    # the same step as two launches on a copy of the cache (linear_ln takes 16-byte aligned rows)
+    tc2 = torch.from_numpy(cache).cuda()
+    qkv = tc2[(n_keys - 1) * B:]
+    rt.linear_ln(torch.from_numpy(np.ascontiguousarray(x[:, :Dm])).cuda(), Dm, 1e-5, tw, tb, None, 0, qkv, ldc, B,
+                 3 * Dm, Dm)
+    out2 = torch.full((B, ldo), -5.0, device="cuda")
+    rt.attn_decode(qkv, tc2[:, Dm:], tc2[:, 2 * Dm:], out2, 1 / 8, ldc, 64, ldc, 64, B * ldc, ldc, 64, B * ldc, ldo,
+                   64, n_keys, B, H, 64)
+    torch.cuda.synchronize()
+    assert fp64.rel_fro(got[:, :Dm], out2.cpu().numpy()[:, :Dm]) <= 2e-6
+
+
+def test_decode_layer_refuses_unsupported_shapes():
+    x, w, b, cache, Dm, ldc = _decode_layer_case(4, 4, 8, 0, seed=1)
+    tx, tw, tc = (torch.from_numpy(t).cuda() for t in (x, w, cache))
+    out = torch.empty((4, Dm), device="cuda")
+    # head_dim 32; more keys than the kernel holds; d_model not a multiple of 256; x rows off a
+    # 16-byte boundary
+    for args in ((8, 4, 4, 32, 128, Dm), (257, 4, 4, 64, 256, Dm), (8, 4, 3, 64, 192, Dm), (8, 3, 4, 64, 256, Dm + 1)):
+        n_keys, B, H, hd, dm, ldx = args
+        with pytest.raises(rt.MI355XError) as e:
+            rt.decode_layer(tx, ldx, 1e-5, tw, None, torch.zeros((300 * 4, ldc), device="cuda"), ldc, out, Dm, 1 / 8,
+                            n_keys, B, H, hd, dm)
+        assert e.value.code == rt.EUNSUPPORTED
+
+
+def test_fused_and_unfused_decode_give_the_same_tokens():
+    """TinyGPT with and without the fused decode step: the same greedy tokens, each equal to the
+    float64 model's except at a near-tie."""
+    w = tinygpt.init_weights(seed=0)
+    prompts = tinygpt.seeded_prompts(batch=16, length=32, seed=11)
+    fused = tinygpt.TinyGPT(w, batch=16).generate(prompts, 40, graph=False)
+    plain = tinygpt.TinyGPT(w, batch=16, fused_decode=False).generate(prompts, 40, graph=False)
+    want, margins = tinygpt64.generate(w, prompts, 40)
+    for got in (fused, plain):
+        for seq, pos, margin in tinygpt64.first_divergence(got, want, margins, 32):
+            assert margin < TAU, (seq, pos, margin)
+    np.testing.assert_array_equal(fused, plain)
+
+
 def test_strided_embedding_and_bad_ids():
     rng = np.random.default_rng(2)
     B, T, D, V = 3, 7, 16, 11

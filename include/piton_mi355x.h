@@ -206,6 +206,18 @@ PITON_API int32_t piton_mi355x_decode_layer(const float *x, int64_t ldx, float e
                                             int64_t ldo, float sm_scale, int64_t n_keys, int64_t batch,
                                             int64_t n_heads, int32_t head_dim, int64_t d_model, void *stream);
 
+/* The decoder's last step in one launch, one workgroup per row m < M: logits[m] = LN(x[m]) W
+ * (+ bias), LN as in piton_mi355x_linear_ln, W [K, N] row-major, bias and logits nullable, and
+ * next[m] = the first index of the largest of the first n_classes logits (numpy's argmax: a NaN
+ * wins). Equal to piton_mi355x_linear_ln followed by piton_mi355x_argmax_rows to rounding. Needs
+ * K a multiple of 256 and N a multiple of 4, both up to 1024, x rows and W 16-byte aligned;
+ * otherwise PITON_EUNSUPPORTED. No reference counterpart: it serves the decoder's greedy step
+ * (the reference has no decoder; its argmax rule is the digits driver's,
+ * examples/digits_model.py:139). */
+PITON_API int32_t piton_mi355x_lm_head_argmax(const float *x, int64_t ldx, float eps, const float *w,
+                                              const float *bias, float *logits, int64_t ldl, int32_t *next,
+                                              int64_t M, int64_t N, int64_t K, int32_t n_classes, void *stream);
+
 /* ---- the perf suite's primitives (perf/suite.py:323-351): elementwise over n elements ---- */
 
 /* out = x. Replaces copy_kernel (examples/primitive_kernels.py:12-17). */

@@ -96,6 +96,18 @@ static inline PhaseRecord *phase_slot() { return nullptr; }
 constexpr uint32_t kPhaseSoftmaxRows = 1, kPhaseSoftmaxWg = 2, kPhaseAttnFast = 3, kPhaseAttnDecodeShort = 4,
                    kPhaseDecodeLayer = 5;
 
+// numpy's argmax rule on (value, index) pairs: a NaN beats any number, the larger value beats
+// the smaller, equal values and two NaNs go to the lower index. The combine is associative and
+// commutative, so a reduction in any order gives the first index of the maximum.
+__device__ __forceinline__ void argmax_combine(float &v, int &i, float v2, int i2) {
+    const bool n1 = v != v, n2 = v2 != v2;
+    const bool take = (n1 && n2) ? i2 < i : n2 ? true : n1 ? false : (v2 > v || (v2 == v && i2 < i));
+    if (take) {
+        v = v2;
+        i = i2;
+    }
+}
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 

@@ -762,17 +762,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
 
 // First index of the largest of x[r, 0:n] (numpy argmax rule: the first NaN wins), one wave
 // per row: each lane scans elements lane, lane + 64, ..., then the (value, index) pairs combine
-// across the wave. The combine (a NaN beats any number, the larger value beats the smaller,
-// equal values and two NaNs go to the lower index) is associative and commutative, so the
-// result is the global first maximum whatever the order.
-__device__ __forceinline__ void argmax_combine(float &v, int &i, float v2, int i2) {
-    const bool n1 = v != v, n2 = v2 != v2;
-    const bool take = (n1 && n2) ? i2 < i : n2 ? true : n1 ? false : (v2 > v || (v2 == v && i2 < i));
-    if (take) {
-        v = v2;
-        i = i2;
-    }
-}
+// across the wave with argmax_combine (common.h), whose result does not depend on the order.
 
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int64_t rows, int64_t ld, int n, int32_t *out) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);

@@ -104,15 +104,6 @@ __device__ __forceinline__ void mlp_load_weights(const float *w, float (&wr)[P][
     }
 }
 
-__device__ __forceinline__ void mlp_argmax_combine(float &v, int &i, float v2, int i2) {
-    const bool n1 = v != v, n2 = v2 != v2;
-    const bool take = (n1 && n2) ? i2 < i : n2 ? true : n1 ? false : (v2 > v || (v2 == v && i2 < i));
-    if (take) {
-        v = v2;
-        i = i2;
-    }
-}
-
 __global__ __launch_bounds__(256) void mlp3_kernel(const float *x, int64_t M, const float *w1, const float *b1,
                                                    const float *w2, const float *b2, const float *w3, const float *b3,
                                                    int k0, int n1, int n2, int n3, float *logits, int32_t *pred,
@@ -142,7 +133,7 @@ __global__ __launch_bounds__(256) void mlp3_kernel(const float *x, int64_t M, co
     if (t < MLP_ROWS && r0 + t < M && pred) {
         float bv = -INFINITY;
         int bi = 0x7FFFFFFF;
-        for (int c = 0; c < n_classes; c++) mlp_argmax_combine(bv, bi, buf[1][t][c], c);
+        for (int c = 0; c < n_classes; c++) argmax_combine(bv, bi, buf[1][t][c], c);
         pred[r0 + t] = bi;
     }
 }
@@ -192,7 +183,7 @@ void mlp3_fixed_kernel(const float *x, int64_t M, const float *w1, const float *
         int bi = 0x7FFFFFFF;
 #pragma unroll
         for (int c = 0; c < N3; c++)
-            if (c < n_classes) mlp_argmax_combine(bv, bi, lv[c], c);
+            if (c < n_classes) argmax_combine(bv, bi, lv[c], c);
         pred[r0 + t] = bi;
     }
 }

@@ -63,6 +63,7 @@ SIGNATURES = {
     "piton_mi355x_attn_fwd_batched": [_p, _p, _p, _p, _f32] + [_i64] * 16 + [_i32, _i32, _p],
     "piton_mi355x_attn_decode": [_p, _p, _p, _p, _f32] + [_i64] * 13 + [_i32, _p],
     "piton_mi355x_decode_layer": [_p, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _f32, _i64, _i64, _i64, _i32, _i64, _p],
+    "piton_mi355x_lm_head_argmax": [_p, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i32, _p],
     "piton_mi355x_copy": [_p, _p, _i64, _p],
     "piton_mi355x_mfma_probe": [_p, _i64, _i32, _p],
     "piton_mi355x_mul": [_p, _p, _p, _i64, _p],
@@ -354,6 +355,20 @@ def decode_layer(x, ldx, eps, w, bias, cache, ldc, out, ldo, sm_scale, n_keys, b
     check_tensor("out", out, max_offset=_span((batch, ldo), (d_model, 1)))
     _call("piton_mi355x_decode_layer", _ptr(x), ldx, float(eps), _ptr(w), _ptr(bias), _ptr(cache), ldc, _ptr(out),
           ldo, float(sm_scale), n_keys, batch, heads, int(head_dim), d_model, _stream())
+
+
+def lm_head_argmax(x, ldx, eps, w, bias, logits, ldl, next_ids, M, N, K, n_classes):
+    """The decoder's last step in one launch, one workgroup per row: logits[m] = LN(x[m]) W
+    (+ bias) (logits nullable) and next_ids[m] = numpy's argmax of the first n_classes logits.
+    Equal to linear_ln + argmax_rows to rounding (K a multiple of 256 and N of 4, both up to
+    1024, 16-byte x rows; else MI355XError with status -2)."""
+    check_tensor("x", x, max_offset=_span((M, ldx), (K, 1)))
+    check_tensor("w", w, max_offset=K * N - 1)
+    check_tensor("bias", bias, max_offset=N - 1, allow_none=True)
+    check_tensor("logits", logits, max_offset=_span((M, ldl), (N, 1)), allow_none=True)
+    check_tensor("next_ids", next_ids, dtype=torch.int32, max_offset=M - 1)
+    _call("piton_mi355x_lm_head_argmax", _ptr(x), ldx, float(eps), _ptr(w), _ptr(bias), _ptr(logits), ldl,
+          _ptr(next_ids), M, N, K, int(n_classes), _stream())
 
 
 # ---- the perf suite's primitives (perf/suite.py:323-351) -----------------------------------

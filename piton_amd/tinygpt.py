@@ -76,9 +76,10 @@ class TinyGPT:
 
     def __init__(self, weights: dict, cfg: Config = Config(), batch: int = 64, device="cuda",
                  fused_decode: bool = True):
-        """fused_decode: decode steps run each layer's layernorm, QKV projection and attention
-        as one piton_mi355x_decode_layer launch where the shapes allow (head_dim 64), instead
-        of linear_ln + attn_decode."""
+        """fused_decode: where the shapes allow, a decode step runs each layer's layernorm, QKV
+        projection and attention as one piton_mi355x_decode_layer launch (head_dim 64) instead
+        of linear_ln + attn_decode, and every forward ends with one piton_mi355x_lm_head_argmax
+        launch instead of linear_ln + argmax_rows."""
         self.cfg, self.B = cfg, batch
         self.fused_decode = fused_decode
         self.w = {k: torch.as_tensor(np.ascontiguousarray(v)).to(device) for k, v in weights.items()}
@@ -141,12 +142,17 @@ class TinyGPT:
                 rt.linear(h, D, w("w1"), w("b1"), None, 0, mlp, F, n, F, D, relu=True)
             rt.linear(mlp, F, w("w2"), w("b2"), x, D, x, D, n, D, F)
         last = (p1 - 1) * B
+        nxt = self.tokens[p1 * B:(p1 + 1) * B]
+        if self.fused_decode and D % 256 == 0 and D <= 1024 and V % 4 == 0 and V <= 1024:
+            # layernorm, LM head and argmax in one launch
+            rt.lm_head_argmax(self.x[last:last + B], D, cfg.eps, self.w["lm"], None, self.logits, V, nxt, B, V, D, V)
+            return
         if B <= 64 and D % 256 == 0:
             rt.linear_ln(self.x[last:last + B], D, cfg.eps, self.w["lm"], None, None, 0, self.logits, V, B, V, D)
         else:
             rt.layernorm(self.x[last:last + B], self.h[last:last + B], D, cfg.eps, B, D)
             rt.linear(self.h[last:last + B], D, self.w["lm"], None, None, 0, self.logits, V, B, V, D)
-        rt.argmax_rows(self.logits, B, V, V, self.tokens[p1 * B:(p1 + 1) * B])
+        rt.argmax_rows(self.logits, B, V, V, nxt)
 
     def _decode(self, T0: int, steps: int, kv_cache: bool):
         self._forward(0, T0)

@@ -280,6 +280,55 @@ def test_decode_layer_refuses_unsupported_shapes():
         assert e.value.code == rt.EUNSUPPORTED
 
 
+@pytest.mark.parametrize("M,N,K,n_classes,with_bias", [(64, 256, 256, 256, False), (3, 1024, 1024, 1000, True),
+                                                       (5, 12, 512, 10, True), (64, 300, 256, 300, False)])
+def test_lm_head_argmax_matches_float64_and_the_two_launches(M, N, K, n_classes, with_bias):
+    """The decoder's last step (layernorm, LM head, argmax) in one launch: logits within float32
+    tolerance of float64, padding untouched, the token equal to numpy's argmax of the kernel's
+    own logits (first index of the maximum; a NaN row gives 0) and to float64's where its top-2
+    margin exceeds TAU, and to linear_ln + argmax_rows."""
+    rng = np.random.default_rng(M + N + K)
+    x = (rng.standard_normal((M, K + 4)) * 3 - 1).astype(np.float32)
+    w = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.2).astype(np.float32) if with_bias else None
+    if M > 1:
+        x[1, 7] = np.nan  # row 1: every logit NaN, token 0
+    tx, tw = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    tb = torch.from_numpy(b).cuda() if with_bias else None
+    logits = torch.full((M, N + 3), -7.0, device="cuda")
+    nxt = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    rt.lm_head_argmax(tx, K + 4, 1e-5, tw, tb, logits, N + 3, nxt, M, N, K, n_classes)
+    torch.cuda.synchronize()
+    got, tok = logits.cpu().numpy(), nxt.cpu().numpy()
+    ref = tinygpt64.layernorm(x[:, :K].astype(np.float64), 1e-5) @ w + (0 if b is None else b)
+    ok = np.isfinite(ref).all(axis=1)
+    assert fp64.rel_fro(got[ok, :N], ref[ok]) <= 2e-6
+    assert np.isnan(got[~ok, :N]).all() and (tok[~ok] == 0).all()
+    assert (got[:, N:] == -7.0).all()
+    np.testing.assert_array_equal(tok, np.argmax(got[:, :n_classes], axis=1))
+    top2 = np.sort(ref[ok, :n_classes], axis=1)[:, -2:]
+    clear = top2[:, 1] - top2[:, 0] > TAU
+    np.testing.assert_array_equal(tok[ok][clear], np.argmax(ref[ok, :n_classes], axis=1)[clear])
+    if M <= 64:
+        y = torch.empty((M, N), device="cuda")
+        xa = torch.from_numpy(np.ascontiguousarray(x[:, :K])).cuda()
+        rt.linear_ln(xa, K, 1e-5, tw, tb, None, 0, y, N, M, N, K)
+        two = torch.empty(M, dtype=torch.int32, device="cuda")
+        rt.argmax_rows(y, M, N, n_classes, two)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(tok[ok][clear], two.cpu().numpy()[ok][clear])
+
+
+def test_lm_head_argmax_refuses_unsupported_shapes():
+    x = torch.zeros((4, 1032), device="cuda")
+    w = torch.zeros((1032 * 1032,), device="cuda")
+    nxt = torch.zeros(4, dtype=torch.int32, device="cuda")
+    for N, K, ldx in ((256, 300, 1032), (1028, 256, 1032), (256, 256, 257)):
+        with pytest.raises(rt.MI355XError) as e:
+            rt.lm_head_argmax(x, ldx, 1e-5, w, None, None, 0, nxt, 2, N, K, N)
+        assert e.value.code == rt.EUNSUPPORTED
+
+
 def test_fused_and_unfused_decode_give_the_same_tokens():
     """TinyGPT with and without the fused decode step: the same greedy tokens, each equal to the
     float64 model's except at a near-tie."""

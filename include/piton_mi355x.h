@@ -198,13 +198,17 @@ PITON_API int32_t piton_mi355x_attn_decode(const float *q, const float *k, const
  * stride ldc), and out[b, h*64 .. h*64+63] gets head h's attention of that q over the keys
  * 0 .. n_keys-1 of the position-major cache (row t * batch + b: k at column d_model + h*64, v at
  * 2 d_model + h*64). Equal to piton_mi355x_linear_ln followed by piton_mi355x_attn_decode to
- * rounding. Needs head_dim 64, d_model = n_heads * 64 a multiple of 256 up to 1024, n_keys <= 256,
- * W and the cache 16-byte aligned with ldc % 4 == 0; otherwise PITON_EUNSUPPORTED. No reference
- * counterpart (the reference has no decoder): it serves the decoder's per-token steps. */
-PITON_API int32_t piton_mi355x_decode_layer(const float *x, int64_t ldx, float eps, const float *w,
-                                            const float *bias, float *cache, int64_t ldc, float *out,
-                                            int64_t ldo, float sm_scale, int64_t n_keys, int64_t batch,
-                                            int64_t n_heads, int32_t head_dim, int64_t d_model, void *stream);
+ * rounding. With ids (nullable; the first layer of a step) x[b] is first set to
+ * tok[ids[b]] + pos (tok [vocab, d_model], pos one row of d_model), as piton_mi355x_embedding
+ * does: an id outside [0, vocab) gives a NaN row and *err = 1 (err nullable). Needs head_dim 64,
+ * d_model = n_heads * 64 a multiple of 256 up to 1024, n_keys <= 256, x, W, the cache, tok and
+ * pos 16-byte aligned with ldx % 4 == 0 and ldc % 4 == 0; otherwise PITON_EUNSUPPORTED. No
+ * reference counterpart (the reference has no decoder): it serves the decoder's per-token steps. */
+PITON_API int32_t piton_mi355x_decode_layer(float *x, int64_t ldx, float eps, const float *w, const float *bias,
+                                            float *cache, int64_t ldc, float *out, int64_t ldo, float sm_scale,
+                                            int64_t n_keys, int64_t batch, int64_t n_heads, int32_t head_dim,
+                                            int64_t d_model, const int32_t *ids, const float *tok,
+                                            const float *pos, int64_t vocab, int32_t *err, void *stream);
 
 /* The decoder's last step in one launch, one workgroup per row m < M: logits[m] = LN(x[m]) W
  * (+ bias), LN as in piton_mi355x_linear_ln, W [K, N] row-major, bias and logits nullable, and

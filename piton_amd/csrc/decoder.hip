@@ -47,7 +47,7 @@ constexpr int kDlMaxModel = 1024;  // d_model
 constexpr int kDlThreads = 512, kDlWaves = kDlThreads / 64;
 
 struct DecodeLayerArgs {
-    const float *x;  // the new rows, row b at x + b * ldx
+    float *x;  // the new rows, row b at x + b * ldx (written with ids)
     int64_t ldx;
     float eps;
     const float *w;     // [d_model, 3 d_model] row-major
@@ -58,6 +58,12 @@ struct DecodeLayerArgs {
     int64_t ldo;
     float scale;  // sm_scale * log2(e)
     int n_keys, batch, n_heads, d_model;
+    // with ids (the first layer of a step): x[b] = tok[ids[b]] + pos, written to x by the
+    // workgroups of head 0; an id outside [0, vocab) gives a NaN row and *err = 1
+    const int32_t *ids;
+    const float *tok, *pos;
+    int64_t vocab;
+    int32_t *err;
     PhaseRecord *phase;  // the launch's phase-trace records (diagnostics builds; null otherwise)
 };
 
@@ -123,6 +129,24 @@ __device__ __forceinline__ void ln_row_store(const f32x4 (&xv)[kLnChunks], int K
             for (int e = 0; e < 4; e++) y[e] = (xv[i][e] - mean) * inv_sd;
             *reinterpret_cast<f32x4 *>(&lnx[4 * lane + 256 * i]) = y;
         }
+}
+
+// The embedding of token `id` at a position instead of a stored row (same chunks as ln_row_load):
+// tok[id] + pos, a NaN row for an id outside [0, vocab). The loads are unconditional (an id
+// outside the vocabulary reads row 0 and is replaced afterwards).
+__device__ __forceinline__ void emb_row_load(const float *tok, const float *pos, int id, int64_t vocab, int K,
+                                             int lane, f32x4 (&xv)[kLnChunks]) {
+    const bool bad = id < 0 || id >= vocab;
+    const f32x4 *tr = reinterpret_cast<const f32x4 *>(tok + (int64_t)(bad ? 0 : id) * K);
+    const f32x4 *pr = reinterpret_cast<const f32x4 *>(pos);
+    const int nx = K / 256;
+#pragma unroll
+    for (int i = 0; i < kLnChunks; i++) {
+        const int c = min(lane + 64 * i, 64 * nx - 1);
+        const f32x4 a = tr[c], p = pr[c];
+#pragma unroll
+        for (int e = 0; e < 4; e++) xv[i][e] = bad ? __int_as_float(0x7FC00000) : a[e] + p[e];
+    }
 }
 
 // A thread's 4 columns of a row-vector x matrix product over a k range of kq rows (kq % 32 == 0):
@@ -237,9 +261,23 @@ __global__ __launch_bounds__(kDlThreads) void decode_layer_kernel(DecodeLayerArg
     f32x4 wa[kRpCh], wb[kRpCh];
     if (!copier) {
         f32x4 xv[kLnChunks];
-        if (wave == 0) ln_row_load(g.x + (int64_t)b * g.ldx, K, lane, xv);
+        const int id = g.ids ? g.ids[b] : 0;  // uniform: one scalar load
+        if (wave == 0) {
+            if (g.ids) emb_row_load(g.tok, g.pos, id, g.vocab, K, lane, xv);
+            else ln_row_load(g.x + (int64_t)b * g.ldx, K, lane, xv);
+        }
         rp_first(wa, wb, wo);
-        if (wave == 0) ln_row_store(xv, K, g.eps, lane, lnx);
+        if (wave == 0) {
+            if (g.ids && h == 0) {
+                // head 0 stores the embedded row for the layer's residual path
+                f32x4 *xr = reinterpret_cast<f32x4 *>(g.x + (int64_t)b * g.ldx);
+#pragma unroll
+                for (int i = 0; i < kLnChunks; i++)
+                    if (i < K / 256) xr[lane + 64 * i] = xv[i];
+                if (lane == 0 && (id < 0 || id >= g.vocab) && g.err) *g.err = 1;
+            }
+            ln_row_store(xv, K, g.eps, lane, lnx);
+        }
     }
     lds_barrier();  // the normalised row is in LDS (the cache copies may still be in flight)
     PITON_PHASE(1);
@@ -423,10 +461,11 @@ __global__ __launch_bounds__(kDlThreads) void lm_head_kernel(LmHeadArgs g) {
 
 PITON_PHASE_TU(decode_layer)
 
-extern "C" int32_t piton_mi355x_decode_layer(const float *x, int64_t ldx, float eps, const float *w,
-                                             const float *bias, float *cache, int64_t ldc, float *out, int64_t ldo,
-                                             float sm_scale, int64_t n_keys, int64_t batch, int64_t n_heads,
-                                             int32_t head_dim, int64_t d_model, void *stream) {
+extern "C" int32_t piton_mi355x_decode_layer(float *x, int64_t ldx, float eps, const float *w, const float *bias,
+                                             float *cache, int64_t ldc, float *out, int64_t ldo, float sm_scale,
+                                             int64_t n_keys, int64_t batch, int64_t n_heads, int32_t head_dim,
+                                             int64_t d_model, const int32_t *ids, const float *tok,
+                                             const float *pos, int64_t vocab, int32_t *err, void *stream) {
     using namespace piton;
     PITON_REQUIRE(n_keys >= 1 && batch >= 0 && n_heads >= 1 && d_model >= 1, PITON_EINVAL,
                   "decode_layer: n_keys=%lld batch=%lld n_heads=%lld d_model=%lld", (long long)n_keys,
@@ -451,11 +490,14 @@ extern "C" int32_t piton_mi355x_decode_layer(const float *x, int64_t ldx, float 
     PITON_REQUIRE(((n_keys + 3) * batch * ldc + 3 * d_model) * 4 < 0x7FFFFFFF, PITON_EUNSUPPORTED,
                   "decode_layer: the cache exceeds 2 GiB");
     PITON_REQUIRE(batch * n_heads <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "decode_layer: too many heads");
+    PITON_REQUIRE(!ids || (tok && pos && vocab >= 1 && aligned16(tok) && aligned16(pos) && aligned4(ids)),
+                  ids && (!tok || !pos || vocab < 1) ? PITON_EINVAL : PITON_EUNSUPPORTED,
+                  "decode_layer: with ids, tok and pos are required (16-byte aligned) and vocab >= 1");
     int rc = require_device();
     if (rc) return rc;
     if (batch == 0) return PITON_OK;
     DecodeLayerArgs g{x, ldx, eps, w, bias, cache, ldc, out, ldo, sm_scale * 1.44269504088896341f,
-                      (int)n_keys, (int)batch, (int)n_heads, (int)d_model, phase_slot()};
+                      (int)n_keys, (int)batch, (int)n_heads, (int)d_model, ids, tok, pos, vocab, err, phase_slot()};
     PITON_LAUNCH(decode_layer_kernel, dim3((unsigned)(batch * n_heads)), dim3(kDlThreads), 0, (hipStream_t)stream, g);
     rc = check_launch("decode_layer");
     if (rc == PITON_OK) clear_error();

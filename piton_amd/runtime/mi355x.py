@@ -62,7 +62,8 @@ SIGNATURES = {
     "piton_mi355x_mlp3": [_p, _i64] + [_p] * 6 + [_i64] * 4 + [_p, _p, _i32, _p],
     "piton_mi355x_attn_fwd_batched": [_p, _p, _p, _p, _f32] + [_i64] * 16 + [_i32, _i32, _p],
     "piton_mi355x_attn_decode": [_p, _p, _p, _p, _f32] + [_i64] * 13 + [_i32, _p],
-    "piton_mi355x_decode_layer": [_p, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _f32, _i64, _i64, _i64, _i32, _i64, _p],
+    "piton_mi355x_decode_layer": [_p, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _f32, _i64, _i64, _i64, _i32, _i64,
+                                  _p, _p, _p, _i64, _p, _p],
     "piton_mi355x_lm_head_argmax": [_p, _i64, _f32, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i32, _p],
     "piton_mi355x_copy": [_p, _p, _i64, _p],
     "piton_mi355x_mfma_probe": [_p, _i64, _i32, _p],
@@ -341,20 +342,28 @@ def attn_decode(q, k, v, out, sm_scale, s_qb, s_qh, s_kb, s_kh, s_kn, s_vb, s_vh
           s_kn, s_vb, s_vh, s_vn, s_ob, s_oh, n_keys, batch, heads, int(head_dim), _stream())
 
 
-def decode_layer(x, ldx, eps, w, bias, cache, ldc, out, ldo, sm_scale, n_keys, batch, heads, head_dim, d_model):
+def decode_layer(x, ldx, eps, w, bias, cache, ldc, out, ldo, sm_scale, n_keys, batch, heads, head_dim, d_model,
+                 ids=None, tok=None, pos=None, vocab=0, err_flag=None):
     """A decode step's layernorm + QKV projection + cache append + attention for one layer, in
     one launch: cache row (n_keys - 1) * batch + b gets LN(x[b]) W + bias (q | k | v), and
     out[b, h*hd:(h+1)*hd] attends head h's query to keys 0 .. n_keys-1 of the position-major
-    cache (rows t * batch + b, k at column d_model + h*hd, v at 2 d_model + h*hd). Equal to
-    linear_ln + attn_decode to rounding (head_dim 64, d_model = heads * 64 a multiple of 256
-    up to 1024, n_keys <= 256; else MI355XError with status -2)."""
+    cache (rows t * batch + b, k at column d_model + h*hd, v at 2 d_model + h*hd). With ids
+    (int32 [batch]), x[b] is first set to tok[ids[b]] + pos (pos: the position's row), as
+    embedding() does. Equal to linear_ln + attn_decode to rounding (head_dim 64, d_model =
+    heads * 64 a multiple of 256 up to 1024, n_keys <= 256; else MI355XError with status -2)."""
     check_tensor("x", x, max_offset=_span((batch, ldx), (d_model, 1)))
     check_tensor("w", w, max_offset=3 * d_model * d_model - 1)
     check_tensor("bias", bias, max_offset=3 * d_model - 1, allow_none=True)
     check_tensor("cache", cache, max_offset=_span((n_keys * batch, ldc), (3 * d_model, 1)))
     check_tensor("out", out, max_offset=_span((batch, ldo), (d_model, 1)))
+    if ids is not None:
+        check_tensor("ids", ids, dtype=torch.int32, max_offset=batch - 1)
+        check_tensor("tok", tok, max_offset=vocab * d_model - 1)
+        check_tensor("pos", pos, max_offset=d_model - 1)
+        check_tensor("err_flag", err_flag, dtype=torch.int32, max_offset=0, allow_none=True)
     _call("piton_mi355x_decode_layer", _ptr(x), ldx, float(eps), _ptr(w), _ptr(bias), _ptr(cache), ldc, _ptr(out),
-          ldo, float(sm_scale), n_keys, batch, heads, int(head_dim), d_model, _stream())
+          ldo, float(sm_scale), n_keys, batch, heads, int(head_dim), d_model, _ptr(ids), _ptr(tok), _ptr(pos),
+          int(vocab), _ptr(err_flag), _stream())
 
 
 def lm_head_argmax(x, ldx, eps, w, bias, logits, ldl, next_ids, M, N, K, n_classes):

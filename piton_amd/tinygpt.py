@@ -104,8 +104,11 @@ class TinyGPT:
         n = (p1 - p0) * B
         r0 = p0 * B
         x, h, att, mlp = (t[r0:r0 + n] for t in (self.x, self.h, self.att, self.mlp))
-        rt.embedding(self.tokens[r0:], 1, B, self.w["tok"], self.w["pos"][p0:], x, D, B * D, B, p1 - p0, D, V, 0,
-                     self.err)
+        # a decode step of the fused path embeds its tokens inside layer 0's decode_layer launch
+        fused_step = p0 > 0 and self.fused_decode and Dh == 64 and D % 256 == 0 and p1 <= 256
+        if not fused_step:
+            rt.embedding(self.tokens[r0:], 1, B, self.w["tok"], self.w["pos"][p0:], x, D, B * D, B, p1 - p0, D, V, 0,
+                         self.err)
         scale = 1.0 / float(np.sqrt(Dh))
         # a decode step's products have at most 64 rows: layernorm fuses into the next linear
         # (the same values bit for bit, one launch instead of two)
@@ -114,9 +117,12 @@ class TinyGPT:
             w = lambda k: self.w[f"{k}{i}"]  # noqa: E731
             cache = self.qkv[i]
             qkv = cache[r0:r0 + n]
-            if p0 > 0 and self.fused_decode and Dh == 64 and D % 256 == 0 and p1 <= 256:
-                # a decode step: layernorm, QKV into the cache row and attention in one launch
-                rt.decode_layer(x, D, cfg.eps, w("wqkv"), w("bqkv"), cache, 3 * D, att, D, scale, p1, B, H, Dh, D)
+            if fused_step:
+                # a decode step: (layer 0: the embedding,) layernorm, QKV into the cache row and
+                # attention in one launch
+                emb = dict(ids=self.tokens[r0:r0 + B], tok=self.w["tok"], pos=self.w["pos"][p0], vocab=V,
+                           err_flag=self.err) if i == 0 else {}
+                rt.decode_layer(x, D, cfg.eps, w("wqkv"), w("bqkv"), cache, 3 * D, att, D, scale, p1, B, H, Dh, D, **emb)
             else:
                 if fuse_ln:
                     rt.linear_ln(x, D, cfg.eps, w("wqkv"), w("bqkv"), None, 0, qkv, 3 * D, n, 3 * D, D)
@@ -131,7 +137,7 @@ class TinyGPT:
             else:
                 if p1 != p0 + 1:
                     raise ValueError("decode steps take one position at a time")
-                if not (self.fused_decode and Dh == 64 and D % 256 == 0 and p1 <= 256):
+                if not fused_step:
                     rt.attn_decode(qkv, cache[:, D:], cache[:, 2 * D:], att, scale, 3 * D, Dh, 3 * D, Dh,
                                    B * 3 * D, 3 * D, Dh, B * 3 * D, D, Dh, p1, B, H, Dh)
             rt.linear(att, D, w("wo"), w("bo"), x, D, x, D, n, D, D)

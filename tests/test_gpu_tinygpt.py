@@ -266,6 +266,46 @@ def test_decode_layer_matches_float64_and_the_two_launches(B, H, n_keys, pad):
     assert fp64.rel_fro(got[:, :Dm], out2.cpu().numpy()[:, :Dm]) <= 2e-6
 
 
+def test_decode_layer_embeds_the_first_layer_like_the_embedding():
+    """With token ids the decode step first sets x[b] = tok[id] + pos (written back to x): the
+    same bits as embedding() followed by the step; an id outside the vocabulary gives a NaN row
+    and raises the flag, as embedding() does."""
+    B, H, n_keys, V = 64, 4, 50, 256
+    x, w, b, cache, Dm, ldc = _decode_layer_case(B, H, n_keys, 0, seed=3)
+    rng = np.random.default_rng(9)
+    tok = torch.from_numpy((rng.standard_normal((V, Dm)) * 0.5).astype(np.float32)).cuda()
+    pos = torch.from_numpy((rng.standard_normal((8, Dm)) * 0.5).astype(np.float32)).cuda()
+    ids = torch.from_numpy(rng.integers(0, V, B).astype(np.int32)).cuda()
+    tw, tb = torch.from_numpy(w).cuda(), torch.from_numpy(b).cuda()
+    outs = []
+    for fused in (False, True):
+        tx = torch.full((B, Dm), 3.0, device="cuda")
+        tc = torch.from_numpy(cache).cuda()
+        out = torch.empty((B, Dm), device="cuda")
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        if fused:
+            rt.decode_layer(tx, Dm, 1e-5, tw, tb, tc, ldc, out, Dm, 1 / 8, n_keys, B, H, 64, Dm, ids=ids, tok=tok,
+                            pos=pos[5], vocab=V, err_flag=err)
+        else:
+            rt.embedding(ids, 1, 1, tok, pos[5:], tx, Dm, Dm, B, 1, Dm, V, 0, err)
+            rt.decode_layer(tx, Dm, 1e-5, tw, tb, tc, ldc, out, Dm, 1 / 8, n_keys, B, H, 64, Dm)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        outs.append([t.cpu().numpy() for t in (tx, tc, out)])
+    for a, c in zip(*outs):
+        np.testing.assert_array_equal(a.view(np.uint32), c.view(np.uint32))
+    ids[3] = V  # outside the vocabulary
+    tx = torch.zeros((B, Dm), device="cuda")
+    out = torch.empty((B, Dm), device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rt.decode_layer(tx, Dm, 1e-5, tw, tb, torch.from_numpy(cache).cuda(), ldc, out, Dm, 1 / 8, n_keys, B, H, 64, Dm,
+                    ids=ids, tok=tok, pos=pos[5], vocab=V, err_flag=err)
+    torch.cuda.synchronize()
+    got_x, got = tx.cpu().numpy(), out.cpu().numpy()
+    assert int(err.item()) == 1 and np.isnan(got_x[3]).all() and np.isnan(got[3]).all()
+    assert np.isfinite(np.delete(got, 3, axis=0)).all()
+
+
 def test_decode_layer_refuses_unsupported_shapes():
     x, w, b, cache, Dm, ldc = _decode_layer_case(4, 4, 8, 0, seed=1)
     tx, tw, tc = (torch.from_numpy(t).cuda() for t in (x, w, cache))

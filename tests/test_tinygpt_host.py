@@ -63,9 +63,51 @@ class HostABI:
     def argmax_rows(x, rows, ld, n, out):
         out[:rows].copy_(torch.argmax(view(x, (rows, n), (ld, 1)), 1).int())
 
+    # the fused entries (piton_mi355x_decode_layer, _lm_head_argmax)
 
-def run_host(monkeypatch, kv_cache, steps=6, batch=3):
-    cfg = tinygpt.Config(d_model=64, n_heads=2, d_mlp=96, vocab=29, context=24, n_layers=2)
+    @staticmethod
+    def _ln(x, eps):
+        d = x - x.mean(1, keepdim=True)
+        return d / torch.sqrt((d * d).mean(1, keepdim=True) + eps)
+
+    @staticmethod
+    def decode_layer(x, ldx, eps, w, bias, cache, ldc, out, ldo, scale, n_keys, batch, heads, dh, d_model, ids=None,
+                     tok=None, pos=None, vocab=0, err_flag=None):
+        xv = view(x, (batch, d_model), (ldx, 1))
+        if ids is not None:
+            xv.copy_(tok[ids.long()] + pos[None])
+        y = HostABI._ln(xv.double(), eps) @ w.double()
+        if bias is not None:
+            y = y + bias.double()
+        rows = view(cache, (n_keys, batch, 3 * d_model), (batch * ldc, ldc, 1))
+        rows[n_keys - 1].copy_(y)
+        q = rows[n_keys - 1, :, :d_model].double().reshape(batch, heads, 1, dh)
+        k = rows[:, :, d_model:2 * d_model].double().reshape(n_keys, batch, heads, dh).permute(1, 2, 0, 3)
+        v = rows[:, :, 2 * d_model:].double().reshape(n_keys, batch, heads, dh).permute(1, 2, 0, 3)
+        p = torch.softmax(q @ k.transpose(-1, -2) * scale, -1)
+        view(out, (batch, d_model), (ldo, 1)).copy_((p @ v)[:, :, 0].reshape(batch, d_model))
+
+    @staticmethod
+    def linear_ln(x, ldx, eps, w, bias, residual, ldr, y, ldy, M, N, K, relu=False):
+        xn = HostABI._ln(view(x, (M, K), (ldx, 1)).double(), eps)
+        HostABI.linear(xn.contiguous(), K, w, bias, residual, ldr, y, ldy, M, N, K, relu)
+
+    @staticmethod
+    def lm_head_argmax(x, ldx, eps, w, bias, logits, ldl, nxt, M, N, K, n_classes):
+        r = HostABI._ln(view(x, (M, K), (ldx, 1)).double(), eps) @ w.double()
+        if bias is not None:
+            r = r + bias.double()
+        if logits is not None:
+            view(logits, (M, N), (ldl, 1)).copy_(r)
+        nxt[:M].copy_(torch.argmax(r[:, :n_classes], 1).int())
+
+
+def run_host(monkeypatch, kv_cache, steps=6, batch=3, fused_shapes=False):
+    """fused_shapes: d_model 256 in heads of 64 and a vocabulary of 32, so that the decoder takes
+    its fused entries (decode_layer with the embedding, lm_head_argmax); otherwise the shapes
+    only the separate entries take (heads of 32, a vocabulary of 29)."""
+    cfg = (tinygpt.Config(d_model=256, n_heads=4, d_mlp=96, vocab=32, context=24, n_layers=2) if fused_shapes else
+           tinygpt.Config(d_model=64, n_heads=2, d_mlp=96, vocab=29, context=24, n_layers=2))
     w = tinygpt.init_weights(cfg, seed=1)
     w = {k: (v * 10 if k.startswith("w") or k == "lm" else v) for k, v in w.items()}  # wide margins
     prompts = tinygpt.seeded_prompts(batch=batch, length=5, vocab=cfg.vocab, seed=2)
@@ -74,7 +116,7 @@ def run_host(monkeypatch, kv_cache, steps=6, batch=3):
     for name in ("x", "h", "att", "mlp", "qkv", "logits"):  # float64 buffers: exact layout check
         setattr(model, name, getattr(model, name).double())
     got = model.generate(prompts, steps, kv_cache=kv_cache)
-    want, _ = tinygpt64.generate(w, prompts, steps, n_layers=2, n_heads=2)
+    want, _ = tinygpt64.generate(w, prompts, steps, n_layers=2, n_heads=cfg.n_heads)
     return got, want
 
 
@@ -86,3 +128,15 @@ def test_driver_layout_kv_cache(monkeypatch):
 def test_driver_layout_recompute(monkeypatch):
     got, want = run_host(monkeypatch, False)
     np.testing.assert_array_equal(got, want)
+
+
+def test_driver_layout_fused_entries(monkeypatch):
+    """The same check through the fused entries (their pointers, strides and the cache row a
+    decode step writes), with the recompute path as the second opinion."""
+    calls = []
+    for name in ("decode_layer", "lm_head_argmax"):
+        f = getattr(HostABI, name)
+        monkeypatch.setattr(HostABI, name, staticmethod(lambda *a, _f=f, _n=name, **k: (calls.append(_n), _f(*a, **k))[1]))
+    got, want = run_host(monkeypatch, True, fused_shapes=True)
+    np.testing.assert_array_equal(got, want)
+    assert {"decode_layer", "lm_head_argmax"} <= set(calls)

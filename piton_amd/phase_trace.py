@@ -140,9 +140,9 @@ def decode_phases(n_keys: int, batch: int = 64, heads: int = 4, d_head: int = 64
 
 def decode_layer_phases(n_keys: int, batch: int = 64, heads: int = 4, d_head: int = 64, launches: int = 12):
     """TinyGPT's fused decode step of a layer (piton_mi355x_decode_layer): per launch, medians
-    over waves of the layernorm phase (to the barrier after it), of the projection on waves 0-2
-    and of the cache copies on wave 3 (both from that barrier), and of the attention after the
-    two meet."""
+    over waves of the layernorm phase (to the barrier after it), of the projection on waves 0-5
+    and of the cache copies on waves 6 and 7 (both from that barrier), and of the attention after
+    the two meet."""
     import torch
 
     from .runtime import mi355x as rt
@@ -158,8 +158,9 @@ def decode_layer_phases(n_keys: int, batch: int = 64, heads: int = 4, d_head: in
     for k in range(1, len(per) - 1):
         ls = per[k]
         t0 = min(r[0] for r in ls)
-        proj = [r for r in ls if (r[4] >> 32) % 4 != 3]
-        copy = [r for r in ls if (r[4] >> 32) % 4 == 3]
+        # the record's wave index is blockIdx.x * 8 + wave: waves 0-5 project, 6 and 7 copy the cache
+        proj = [r for r in ls if (r[4] >> 32) % 8 < 6]
+        copy = [r for r in ls if (r[4] >> 32) % 8 >= 6]
         rows.append(dict(layernorm=statistics.median(r[1] - r[0] for r in ls),
                          projection=statistics.median(r[2] - r[1] for r in proj),
                          cache_copies=statistics.median(r[2] - r[1] for r in copy),
@@ -197,7 +198,7 @@ def main():
               f"{us(m['first_data'])} (K, V in) | {us(m['wave_wait'])} | {us(m['end'])} | {us(m['gap_to_next'])} | "
               f"per wave: scores and max {us(m['loop'])}, exp, sum, P V {us(m['merge'])} |")
     print()
-    print("| fused decode step, 64 x 4 heads x 64 | layernorm | projection (waves 0-2) | cache copies (wave 3) | "
+    print("| fused decode step, 64 x 4 heads x 64 | layernorm | projection (waves 0-5) | cache copies (waves 6, 7) | "
           "attention | last wave ends | gap to next launch |")
     print("|---|---|---|---|---|---|---|")
     for nk in (96, 160):

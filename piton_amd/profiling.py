@@ -47,7 +47,7 @@ TIMED = "matmul 4096^3"  # the workload of bench.py's timed region
 
 
 def short(name: str) -> str:
-    name = name.split("(")[0]
+    name = name.replace("(anonymous namespace)::", "").split("(")[0]
     name = re.sub(r"^void ", "", name)
     return name.replace("piton::", "")
 

@@ -984,9 +984,10 @@ static int attn_check(const float *q, const float *k, const float *v, const floa
                   "attn_fwd: null pointer");
     PITON_REQUIRE(aligned4(q) && aligned4(k) && aligned4(v) && aligned4(out), PITON_EINVAL,
                   "attn_fwd: pointers must be 4-byte aligned");
-    PITON_REQUIRE(batch * n_heads * ((n_ctx + 31) / 32) <= 0x7FFFFFFF, PITON_EUNSUPPORTED,
-                  "attn_fwd: %lld heads x N_CTX %lld exceed one grid", (long long)(batch * n_heads), (long long)n_ctx);
     PITON_REQUIRE(n_ctx < (1LL << 31) - 64, PITON_EUNSUPPORTED, "attn_fwd: N_CTX %lld too large", (long long)n_ctx);
+    PITON_REQUIRE(sat_mul(sat_mul(batch, n_heads), (n_ctx + 31) / 32) <= 0x7FFFFFFF, PITON_EUNSUPPORTED,
+                  "attn_fwd: %lld x %lld heads x N_CTX %lld exceed one grid", (long long)batch, (long long)n_heads,
+                  (long long)n_ctx);
     return PITON_OK;
 }
 
@@ -1046,8 +1047,8 @@ int32_t piton_mi355x_attn_decode(const float *q, const float *k, const float *v,
                   (long long)n_keys, kMaxDecodeKeys);
     PITON_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, PITON_EUNSUPPORTED,
                   "attn_decode: HEAD_DIM %d not in {16, 32, 64, 128}", head_dim);
-    PITON_REQUIRE(batch * n_heads == 0 || (q && k && v && out), PITON_EINVAL, "attn_decode: null pointer");
-    PITON_REQUIRE(batch * n_heads <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "attn_decode: too many heads");
+    PITON_REQUIRE(batch == 0 || n_heads == 0 || (q && k && v && out), PITON_EINVAL, "attn_decode: null pointer");
+    PITON_REQUIRE(sat_mul(batch, n_heads) <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "attn_decode: too many heads");
     int rc = require_device();
     if (rc) return rc;
     if (batch * n_heads == 0) return PITON_OK;

@@ -110,6 +110,16 @@ __device__ __forceinline__ void argmax_combine(float &v, int &i, float v2, int i
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+// a * b and a + b for the host's size checks on caller-supplied extents and strides: INT64_MAX
+// where the result overflows, so that a check against any bound fails instead of wrapping
+inline int64_t sat_mul(int64_t a, int64_t b) {
+    int64_t r;
+    return __builtin_mul_overflow(a, b, &r) ? INT64_MAX : r;
+}
+inline int64_t sat_add(int64_t a, int64_t b) {
+    int64_t r;
+    return __builtin_add_overflow(a, b, &r) ? INT64_MAX : r;
+}
 
 #define PITON_REQUIRE(cond, code, ...)                  \
     do {                                                \

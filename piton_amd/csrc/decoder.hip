@@ -487,9 +487,9 @@ extern "C" int32_t piton_mi355x_decode_layer(float *x, int64_t ldx, float eps, c
                   "decode_layer: W, the cache and x need 16-byte alignment (ldc %% 4 == 0, ldx %% 4 == 0)");
     // every cache offset the kernel forms (copies of up to three rows past the last one included)
     // fits 31 bits
-    PITON_REQUIRE(((n_keys + 3) * batch * ldc + 3 * d_model) * 4 < 0x7FFFFFFF, PITON_EUNSUPPORTED,
+    PITON_REQUIRE(sat_mul(sat_mul(n_keys + 3, batch), ldc) < 0x7FFFFFFF / 4 - 3 * d_model, PITON_EUNSUPPORTED,
                   "decode_layer: the cache exceeds 2 GiB");
-    PITON_REQUIRE(batch * n_heads <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "decode_layer: too many heads");
+    PITON_REQUIRE(sat_mul(batch, n_heads) <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "decode_layer: too many heads");
     PITON_REQUIRE(!ids || (tok && pos && vocab >= 1 && aligned16(tok) && aligned16(pos) && aligned4(ids)),
                   ids && (!tok || !pos || vocab < 1) ? PITON_EINVAL : PITON_EUNSUPPORTED,
                   "decode_layer: with ids, tok and pos are required (16-byte aligned) and vocab >= 1");

@@ -976,7 +976,7 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     if (g.s_bn == 1 && g.s_bk > 0) p.bkc = false;
     else if (g.s_bk == 1 && g.s_bn > 0 && g.s_bn % 4 == 0 && g.K % 4 == 0 && aligned16(g.b)) p.bkc = true;
     else return p;
-    auto tiles = [&](int64_t tb) { return ((g.M + tb - 1) / tb) * ((g.N + tb - 1) / tb); };
+    auto tiles = [&](int64_t tb) { return sat_mul((g.M + tb - 1) / tb, (g.N + tb - 1) / tb); };
     const int64_t nk = (g.K + 31) / 32;
 #ifndef PITON_SPLIT_NB_MAX
 #define PITON_SPLIT_NB_MAX 2
@@ -987,8 +987,8 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     while (ks < kMaxSplitWaves && nt * ks < PITON_SPLIT_WAVES_PER_CU * (int64_t)cus && 4 * ks <= nk) ks *= 2;
     // every byte offset a lane forms (the prefetch past the last tile included) stays below 2^31
     const int64_t tb = 32 * nb, kpad = g.K + 32 * (2 * ks + 3);  // the farthest prefetch: tile nk - 1 + 2 ks
-    if (((g.M + tb) * g.s_am + kpad * g.s_ak + 4) * 4 >= (1LL << 31) ||
-        (kpad * g.s_bk + (g.N + tb) * g.s_bn) * 4 >= (1LL << 31) || nt > 0x7FFFFFFF)
+    if (sat_add(sat_mul(g.M + tb, g.s_am), sat_mul(kpad, g.s_ak)) >= (1LL << 29) - 4 ||
+        sat_add(sat_mul(kpad, g.s_bk), sat_mul(g.N + tb, g.s_bn)) >= (1LL << 29) || nt > 0x7FFFFFFF)
         return p;
     p.nb = nb, p.ks = ks, p.tiles = nt;
     return p;
@@ -1050,7 +1050,7 @@ static void launch_direct(bool one_gen, bool wide, bool akc, bool bkc, const Gem
 // the dense entry, whose bits the fused digits chain reproduces, keeps the LDS kernel)
 static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_ok) {
     if (g.M == 0 || g.N == 0) return PITON_OK;
-    const int64_t tiles = ((g.M + GBM - 1) / GBM) * ((g.N + GBN - 1) / GBN);
+    const int64_t tiles = sat_mul((g.M + GBM - 1) / GBM, (g.N + GBN - 1) / GBN);
     PITON_REQUIRE(tiles <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "%s: %lld tiles exceed one grid", what, (long long)tiles);
     // a group taller than the tile rows orders tiles exactly as a group of all of them does;
     // the clamp keeps group_m * num_pid_n within the tile count (no 32-bit overflow in the kernels)
@@ -1068,8 +1068,8 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
     const bool vec_layouts = (al == VEC_ROW || al == VEC_COL) && (bl == VEC_ROW || bl == VEC_COL);
     const bool direct = PITON_GEMM_DIRECT && vec_layouts && g.K > 0 && g.M % DBM == 0 && g.N % DBN == 0 &&
                         g.K % (2 * DKT) == 0 && g.s_am > 0 && g.s_ak > 0 && g.s_bk > 0 && g.s_bn > 0 &&
-                        (g.M - 1) * g.s_am + (g.K - 1) * g.s_ak < (1LL << 29) &&
-                        (g.K - 1) * g.s_bk + (g.N - 1) * g.s_bn < (1LL << 29);
+                        sat_add(sat_mul(g.M - 1, g.s_am), sat_mul(g.K - 1, g.s_ak)) < (1LL << 29) &&
+                        sat_add(sat_mul(g.K - 1, g.s_bk), sat_mul(g.N - 1, g.s_bn)) < (1LL << 29);
     const bool akc = al == VEC_ROW, bkc = bl == VEC_COL;  // the operands contiguous along K
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     // the direct kernel's tiles: 128 x 128, or 128 x 256 when that takes as many generations of

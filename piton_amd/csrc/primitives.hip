@@ -318,7 +318,7 @@ int32_t piton_mi355x_transpose(const float *x, float *out, int64_t n_rows, int64
                   (long long)stride_out, (long long)n_rows);
     PITON_REQUIRE(n_rows == 0 || n_cols == 0 || (x && out), PITON_EINVAL, "transpose: null pointer");
     const int64_t tiles_m = (n_rows + 63) / 64, tiles_n = (n_cols + 63) / 64;
-    PITON_REQUIRE(tiles_m * tiles_n <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "transpose: too large");
+    PITON_REQUIRE(sat_mul(tiles_m, tiles_n) <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "transpose: too large");
     int rc = require_device();
     if (rc) return rc;
     if (n_rows == 0 || n_cols == 0) return PITON_OK;

@@ -88,6 +88,27 @@ def test_invalid_arguments_fail_before_any_device_call():
     assert rc == mi355x.EUNSUPPORTED
 
 
+def test_size_checks_do_not_wrap():
+    """Extents whose products overflow 64 bits are refused, not wrapped past the grid and offset
+    checks (host buffers stand in for device ones: the checks run before any device call)."""
+    L = _raw()
+    null = ctypes.c_void_p(0)
+    buf = np.zeros(4096, np.float32)
+    p = ctypes.c_void_p(buf.ctypes.data)
+    assert buf.ctypes.data % 16 == 0
+    big = 1 << 40
+    # heads x query groups: 2^62 heads x 2 groups
+    rc = L.piton_mi355x_attn_fwd(p, p, p, p, 1.0, *([0] * 9), 64, 1 << 62, 64, 1, null)
+    assert rc == mi355x.EUNSUPPORTED and b"exceed one grid" in L.piton_mi355x_last_error()
+    # tiles: 2^34 x 2^34
+    rc = L.piton_mi355x_transpose(p, p, big, big, big, big, null)
+    assert rc == mi355x.EUNSUPPORTED and b"too large" in L.piton_mi355x_last_error()
+    # cache offsets: (1 + 3) x 2^40 rows x 2^40 floats
+    rc = L.piton_mi355x_decode_layer(p, 256, 1e-5, p, null, p, big, p, 256, 0.125, 1, big, 4, 64, 256,
+                                     null, null, null, 0, null, null)
+    assert rc == mi355x.EUNSUPPORTED and b"2 GiB" in L.piton_mi355x_last_error()
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device path")
 def test_no_device_is_reported():
     with pytest.raises(mi355x.MI355XError) as e:

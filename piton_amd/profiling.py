@@ -12,6 +12,9 @@ calibration add of known size (bench.py CAL_ELEMS: reads 2 x 256 MiB, writes 256
 true bytes. --json writes {workload: {fetch_bytes, write_bytes, ...}}.
 With --mfma, PMC_DIR holds a `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES` run of
 `python3 bench.py --pmc-probe`: the MFMA pipe occupancy of the benchmark's MFMA workloads.
+With --lds, PMC_DIR holds a `--pmc GRBM_GUI_ACTIVE SQ_WAVE_CYCLES SQ_LDS_IDX_ACTIVE
+SQ_LDS_BANK_CONFLICT` run of the same: each workload's mean resident waves per SIMD and its LDS
+bank-conflict cycles per conflict-free LDS cycle.
 """
 from __future__ import annotations
 
@@ -160,6 +163,44 @@ def mfma_busy(pmc_dir, xcds=8, simds=1024):
             for label, w in out.items()}
 
 
+def _per_dispatch(pmc_dir):
+    """{((kernel, grid), dispatch): {counter: value}} for the benchmark launches."""
+    per = {}
+    for r in csv.DictReader(open(_one(os.path.join(pmc_dir, "*_counter_collection.csv")))):
+        key = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
+        if key in LAUNCHES:
+            per.setdefault((key, r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+    return per
+
+
+def lds_occupancy(pmc_dir, xcds=8, cus=256, simds_per_cu=4):
+    """Per benchmark workload, from a `--pmc GRBM_GUI_ACTIVE SQ_WAVE_CYCLES SQ_LDS_IDX_ACTIVE
+    SQ_LDS_BANK_CONFLICT` run (each counter summed over the chip, as rocprofv3 reports them):
+    waves per SIMD = 4 SQ_WAVE_CYCLES (counted in units of 4 cycles) / (GUI cycles per XCD x
+    SIMDs), the time-averaged resident waves, against the kernel's launch limit; LDS conflicts =
+    SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT), the cycles lost to bank
+    conflicts per conflict-free cycle of LDS access (the LdsBankConflict definition of
+    rocprofiler-sdk's counter_defs.yaml for gfx950). Sums over all dispatches of a workload."""
+    out = {}
+    for (key, _), d in _per_dispatch(pmc_dir).items():
+        need = ("GRBM_GUI_ACTIVE", "SQ_WAVE_CYCLES", "SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT")
+        if not all(c in d for c in need):
+            continue
+        w = out.setdefault(LAUNCHES[key][0], dict(kernels=[], dispatches=0, wave=0.0, cycles=0.0, lds=0.0, conf=0.0))
+        if key[0] not in w["kernels"]:
+            w["kernels"].append(key[0])
+        w["dispatches"] += 1
+        w["wave"] += 4 * d["SQ_WAVE_CYCLES"]
+        w["cycles"] += d["GRBM_GUI_ACTIVE"] / xcds * cus * simds_per_cu
+        w["lds"] += d["SQ_LDS_IDX_ACTIVE"]
+        w["conf"] += d["SQ_LDS_BANK_CONFLICT"]
+    return {label: dict(kernel=" + ".join(w["kernels"]), dispatches=w["dispatches"],
+                        waves_per_simd=w["wave"] / w["cycles"],
+                        lds_active=w["lds"], lds_conflict_cycles=w["conf"],
+                        lds_conflict_ratio=w["conf"] / (w["lds"] - w["conf"]) if w["lds"] > w["conf"] else None)
+            for label, w in out.items()}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("kt_dir")
@@ -171,7 +212,19 @@ def main(argv=None):
     ap.add_argument("--commit", default=None, help="the commit the traced runs were made at (recorded)")
     ap.add_argument("--mfma", action="store_true",
                     help="kt_dir is a --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES run: print MFMA occupancy")
+    ap.add_argument("--lds", action="store_true",
+                    help="kt_dir is a --pmc GRBM_GUI_ACTIVE SQ_WAVE_CYCLES SQ_LDS_IDX_ACTIVE SQ_LDS_BANK_CONFLICT run: "
+                         "print resident waves and LDS bank conflicts")
     a = ap.parse_args(argv)
+    if a.lds:
+        sys.stdout.write("| workload | kernel | dispatches | resident waves per SIMD | LDS active cycles "
+                         "| bank-conflict cycles | conflict cycles per conflict-free LDS cycle |\n"
+                         "|---|---|---|---|---|---|---|\n")
+        for label, m in lds_occupancy(a.kt_dir).items():
+            ratio = "—" if m["lds_conflict_ratio"] is None else f"{m['lds_conflict_ratio']:.3f}"
+            sys.stdout.write(f"| {label} | `{m['kernel']}` | {m['dispatches']} | {m['waves_per_simd']:.2f} | "
+                             f"{m['lds_active']:.3g} | {m['lds_conflict_cycles']:.3g} | {ratio} |\n")
+        return
     if a.mfma:
         sys.stdout.write("| workload | kernel | dispatches | MFMA pipe busy |\n|---|---|---|---|\n")
         for label, m in mfma_busy(a.kt_dir).items():

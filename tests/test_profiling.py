@@ -68,3 +68,22 @@ def test_mfma_busy(tmp_path):
     assert list(m) == ["matmul 4096^3"]
     assert m["matmul 4096^3"]["mfma_busy"] == pytest.approx(0.8)
     assert m["matmul 4096^3"]["dispatches"] == 2
+
+
+def test_lds_occupancy(tmp_path):
+    d = str(tmp_path / "pmc")
+    att = "void piton::(anonymous namespace)::attn_fwd_fast<64, true>(piton::AttnArgs)"
+    # 1e5 GUI cycles on each of 8 XCDs; two waves resident on each of the 1024 SIMDs all along
+    # (SQ_WAVE_CYCLES counts units of 4 cycles); LDS active 3e7 cycles chip-wide, 1e7 of them
+    # bank-conflict cycles: 0.5 conflict cycles per conflict-free cycle
+    gui = 8 * 1e5
+    waves = 2 * 1e5 * 1024 / 4
+    write_pmc(d, [(3, att, 131072, "GRBM_GUI_ACTIVE", gui, 0, 1), (3, att, 131072, "SQ_WAVE_CYCLES", waves, 0, 1),
+                  (3, att, 131072, "SQ_LDS_IDX_ACTIVE", 3e7, 0, 1), (3, att, 131072, "SQ_LDS_BANK_CONFLICT", 1e7, 0, 1),
+                  (4, ADD, 1024, "GRBM_GUI_ACTIVE", 100.0, 0, 1)])
+    m = profiling.lds_occupancy(d)
+    assert list(m) == ["attention 32 x 1024 x 64 causal"]
+    a = m["attention 32 x 1024 x 64 causal"]
+    assert a["kernel"] == "attn_fwd_fast<64, true>" and a["dispatches"] == 1
+    assert a["waves_per_simd"] == pytest.approx(2.0)
+    assert a["lds_conflict_ratio"] == pytest.approx(0.5)

@@ -96,6 +96,15 @@ class TinyGPT:
         self.err = torch.zeros(1, dtype=torch.int32, device=device)
         self._graphs = {}  # (T0, steps, kv_cache) -> captured decode
 
+    def decode_layer_fits(self, n_keys: int) -> bool:
+        """Whether a decode step over n_keys cached positions fits the fused decode_layer entry:
+        heads of 64, d_model a multiple of 256 up to 1024, at most 256 keys, and every cache
+        offset of the launch (rows of 3 d_model floats, n_keys + 3 positions of B rows) within
+        31 bits. Other shapes run the separate layernorm, projection and attention launches."""
+        D, B = self.cfg.d_model, self.B
+        return (self.cfg.head_dim == 64 and D % 256 == 0 and D <= 1024 and n_keys <= 256 and
+                (n_keys + 3) * B * 3 * D < 0x7FFFFFFF // 4 - 3 * D)
+
     # -- one forward over positions [p0, p1) ---------------------------------------------------
 
     def _forward(self, p0: int, p1: int):
@@ -105,7 +114,7 @@ class TinyGPT:
         r0 = p0 * B
         x, h, att, mlp = (t[r0:r0 + n] for t in (self.x, self.h, self.att, self.mlp))
         # a decode step of the fused path embeds its tokens inside layer 0's decode_layer launch
-        fused_step = p0 > 0 and self.fused_decode and Dh == 64 and D % 256 == 0 and p1 <= 256
+        fused_step = p0 > 0 and self.fused_decode and self.decode_layer_fits(p1)
         if not fused_step:
             rt.embedding(self.tokens[r0:], 1, B, self.w["tok"], self.w["pos"][p0:], x, D, B * D, B, p1 - p0, D, V, 0,
                          self.err)

@@ -140,3 +140,23 @@ def test_driver_layout_fused_entries(monkeypatch):
     got, want = run_host(monkeypatch, True, fused_shapes=True)
     np.testing.assert_array_equal(got, want)
     assert {"decode_layer", "lm_head_argmax"} <= set(calls)
+
+
+def test_fused_decode_only_where_the_entry_takes_the_shape():
+    """The fused decode step is chosen only for shapes decode_layer accepts (its limits: heads of
+    64, d_model a multiple of 256 up to 1024, at most 256 keys, cache offsets within 31 bits);
+    the rest take the separate launches instead of an unsupported-shape error."""
+    def model(d_model, n_heads, batch):
+        cfg = tinygpt.Config(d_model=d_model, n_heads=n_heads, d_mlp=64, vocab=32, context=8, n_layers=1)
+        m = tinygpt.TinyGPT.__new__(tinygpt.TinyGPT)
+        m.cfg, m.B = cfg, batch
+        return m
+    assert model(256, 4, 64).decode_layer_fits(160)
+    assert model(1024, 16, 64).decode_layer_fits(256)
+    assert not model(256, 4, 64).decode_layer_fits(257)      # more keys than the entry stages
+    assert not model(1280, 20, 64).decode_layer_fits(16)     # d_model past 1024
+    assert not model(256, 8, 64).decode_layer_fits(16)       # heads of 32
+    assert not model(384, 6, 64).decode_layer_fits(16)       # d_model not a multiple of 256
+    # cache offsets: (n_keys + 3) positions x B rows x 3 d_model floats past 2 GiB
+    assert model(1024, 16, 1024).decode_layer_fits(64)
+    assert not model(1024, 16, 1024).decode_layer_fits(256)

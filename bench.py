@@ -329,9 +329,14 @@ def bench_attention(launches=32):
     return line, tuple(t.cpu().numpy() for t in (q, k, v, out))
 
 
+MLP_BATCHES = (1, 16, 64, 256, 1797)
+
+
 def bench_mlp(reps=3):
-    """Digits MLP 64 -> 128 -> 64 -> 10 over a batch of 1797 unnormalised [0, 16] images, one
-    fused launch (three dense layers and the argmax) replayed from a HIP graph."""
+    """Digits MLP 64 -> 128 -> 64 -> 10 over batches of 1, 16, 64, 256 and 1797 unnormalised
+    [0, 16] images (the batches of the reference's latency table), one fused launch (three dense
+    layers and the argmax): `us` per batch from launches replayed back to back from a HIP graph,
+    and `us_call`, the median wall time of one host call (launch and synchronisation)."""
     import numpy as np
     import torch
 
@@ -340,11 +345,29 @@ def bench_mlp(reps=3):
     mlp = digits.MLP(layers, max_batch=1797)
     xh = np.random.default_rng(0).integers(0, 17, (1797, 64)).astype(np.float32)
     x = torch.from_numpy(xh).cuda()
-    avg = timed_graph(lambda i: mlp.run(x), 16, reps)
+    batches = []
+    for m in MLP_BATCHES:
+        xm = x[:m]
+        avg = timed_graph(lambda i: mlp.run(xm), 16, reps)
+        calls = []
+        for _ in range(50):
+            t0 = time.perf_counter()
+            mlp.run(xm)
+            torch.cuda.synchronize()
+            calls.append(time.perf_counter() - t0)
+        batches.append(dict(batch=m, us=round(avg * 1e6, 3), images_per_s=round(m / avg, 1),
+                            us_call=round(sorted(calls)[len(calls) // 2] * 1e6, 1)))
     logits, pred = mlp.run(x)
     torch.cuda.synchronize()
-    line = dict(batch=1797, us=round(avg * 1e6, 3), images_per_s=round(1797 / avg, 1))
+    full = batches[-1]
+    line = dict(batch=1797, us=full["us"], images_per_s=full["images_per_s"], kernel=mlp_kernel_name(),
+                batches=batches)
     return line, (layers, xh, logits.cpu().numpy(), pred.cpu().numpy())
+
+
+def mlp_kernel_name():
+    from piton_amd.runtime import mi355x as rt
+    return rt.last_launches()[0]["kernel"]
 
 
 def bench_tinygpt():
@@ -515,7 +538,9 @@ def cpu_attention(sample, budget_s=1.5):
 
 def cpu_mlp(sample, budget_s=1.0):
     """The oracle's three dense layers (RTZ, the emulator's order) and argmax over the 1797
-    images, numpy float64 for the same chain; the GPU's predictions against the oracle's."""
+    images, numpy float64 for the same chain; the GPU's predictions against the oracle's. Per
+    batch of the reference's latency table: the oracle's time for one batch on one thread and
+    numpy float64's (median of a few runs)."""
     import numpy as np
 
     import oracle
@@ -538,6 +563,25 @@ def cpu_mlp(sample, budget_s=1.0):
     pred_orc = oracle.argmax_rows(orc, 10)
     out["err_vs_fp64"] = dict(gpu=fp64.rel_fro(logits_gpu, h), oracle=fp64.rel_fro(orc, h))
     out["predictions_equal_oracle"] = int((pred_gpu == pred_orc).sum())
+
+    def median_us(fn, reps):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return round(sorted(ts)[len(ts) // 2] * 1e6, 1)
+
+    def f64_chain(xb):
+        hb = xb.astype(np.float64)
+        for w, b, relu in chain:
+            hb = fp64.dense(hb, w, b, relu)
+        return np.argmax(hb[:, :10], axis=1)
+
+    out["batches"] = [dict(batch=m, oracle_1_thread_us=median_us(lambda: oracle.mlp_forward(x[:m], chain),
+                                                                  3 if m < 1797 else 1),
+                           numpy_fp64_us=median_us(lambda: f64_chain(x[:m]), 5))
+                      for m in MLP_BATCHES]
     return out
 
 

@@ -618,7 +618,9 @@ void attn_fwd_fast(AttnArgs g) {
     }
     // the other waves need the Q tiles only: wait for this wave's LDS writes and meet at the
     // barrier, without the release fence of __syncthreads, whose wait covers every memory
-    // operation in flight (the first block's K, which only this wave reads, included)
+    // operation in flight (the first block's K, which only this wave reads, included); the
+    // empty asm with a memory clobber keeps the compiler from moving a Q store below the barrier
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitcntLgkm0);
     __builtin_amdgcn_s_barrier();

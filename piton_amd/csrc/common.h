@@ -94,7 +94,7 @@ static inline PhaseRecord *phase_slot() { return nullptr; }
 #endif
 // kernel ids of the trace records
 constexpr uint32_t kPhaseSoftmaxRows = 1, kPhaseSoftmaxWg = 2, kPhaseAttnFast = 3, kPhaseAttnDecodeShort = 4,
-                   kPhaseDecodeLayer = 5;
+                   kPhaseDecodeLayer = 5, kPhaseMlp = 6;
 
 // numpy's argmax rule on (value, index) pairs: a NaN beats any number, the larger value beats
 // the smaller, equal values and two NaNs go to the lower index. The combine is associative and

@@ -72,8 +72,11 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 // A workgroup barrier for LDS data: this wave's LDS stores are done, then s_barrier. Unlike
 // __syncthreads, whose release fence waits for every memory operation in flight, it lets the
 // cache copies and the global stores (the cache row, which nothing here reads back) stay in
-// flight.
+// flight. The empty asm with a memory clobber keeps the compiler from moving an LDS store below
+// the barrier (the waitcnt and s_barrier builtins do not order memory); a release fence limited
+// to LDS would do the same but also waits for the LDS-DMA cache copies in flight (vmcnt(0)).
 __device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitcntLgkm0);
     __builtin_amdgcn_s_barrier();

@@ -1,16 +1,16 @@
 // The digits MLP chain (examples/digits_model.py:120-139: three dense_layer_kernel launches,
 // examples/nn_kernels.py:23-74, then the argmax of the first ten logits) in one launch.
 //
-// A workgroup of four waves takes 32 rows through all three layers with the activations in
-// LDS: layer l's 32-column output tiles go to waves round-robin, each computed as one
-// v_mfma_f32_32x32x2_f32 chain over the whole K in ascending k pairs -- the order the dense
-// GEMM uses -- then bias, ReLU (hidden layers) and the fp32 store, so the logits are the three
-// dense launches' logits bit for bit. The A operand (the previous layer's rows) comes from LDS
-// (row pitch 257: conflict-free), the B operand (weights, L2-resident after the first
-// workgroups) from memory, a chunk of 32 k pairs loaded ahead of its MFMAs. (Staging all three
-// weight matrices in LDS first measured slower: 24.5 us against 15.9.) The argmax follows
-// numpy's rule (first index of the maximum; a NaN wins), the rule of the dense entry's fused
-// argmax. 1797 rows: 57 workgroups instead of three launches of 15 tiles each.
+// The digits networks (64 -> 128 -> 64 -> 10 or 16) take mlp3_rows16_kernel below: 16 rows per
+// workgroup on 16x16x4 MFMAs. Other sizes take mlp3_kernel: a workgroup of four waves takes 32
+// rows through all three layers with the activations in LDS: layer l's 32-column output tiles go
+// to waves round-robin, each computed as one v_mfma_f32_32x32x2_f32 chain over the whole K in
+// ascending k pairs -- the order the dense GEMM uses -- then bias, ReLU (hidden layers) and the
+// fp32 store, so its logits are the three dense launches' logits bit for bit. The A operand (the
+// previous layer's rows) comes from LDS (row pitch 257: conflict-free), the B operand (weights,
+// L2-resident after the first workgroups) from memory, a chunk of 32 k pairs loaded ahead of
+// its MFMAs. The argmax follows numpy's rule (first index of the maximum; a NaN wins), the rule
+// of the dense entry's fused argmax.
 #include "common.h"
 
 namespace piton {
@@ -57,53 +57,6 @@ __device__ __forceinline__ void mlp_layer(const float (*in)[MLP_PITCH], int k, c
     }
 }
 
-// mlp_layer for a layer whose sizes are known at compile time, with the B operands already in
-// registers: wr[p][u] is weight row 2u + half, column 32*(wave + 4p) + l31 (0 past n). The same
-// MFMA chain and epilogue as mlp_layer, so the same values.
-template <int K, int N, int P>
-__device__ __forceinline__ void mlp_layer_regs(const float (*in)[MLP_PITCH], const float (&wr)[P][K / 2],
-                                               const float *b, bool relu, float (*out)[MLP_PITCH]) {
-    typedef float f32x16 __attribute__((ext_vector_type(16)));
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, l31 = lane & 31;
-#pragma unroll
-    for (int p = 0; p < P; p++) {
-        const int tile = wave + 4 * p;
-        if (tile >= (N + 31) / 32) break;  // wave-uniform
-        const int col = 32 * tile + l31;
-        const bool col_ok = col < N;
-        f32x16 acc;
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[r] = 0.f;
-#pragma unroll
-        for (int u = 0; u < K / 2; u++)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(in[l31][2 * u + half], wr[p][u], acc, 0, 0, 0);
-        const float bias = (b && col_ok) ? b[col] : 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            float v = acc[r];
-            if (b) v += bias;
-            if (relu && v < 0.f) v = 0.f;
-            if (col_ok) out[8 * (r >> 2) + 4 * half + (r & 3)][col] = v;
-        }
-    }
-}
-
-// The wave's B operands of one layer (its tiles wave, wave + 4, ...), requested without waiting
-template <int K, int N, int P>
-__device__ __forceinline__ void mlp_load_weights(const float *w, float (&wr)[P][K / 2]) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, l31 = lane & 31;
-#pragma unroll
-    for (int p = 0; p < P; p++) {
-        const int col = 32 * (wave + 4 * p) + l31;
-        const bool ok = col < N;
-#pragma unroll
-        for (int u = 0; u < K / 2; u++) {
-            const float v = w[(int64_t)(2 * u + half) * N + (ok ? col : 0)];  // unconditional, as in mlp_layer
-            wr[p][u] = ok ? v : 0.f;
-        }
-    }
-}
-
 __global__ __launch_bounds__(256) void mlp3_kernel(const float *x, int64_t M, const float *w1, const float *b1,
                                                    const float *w2, const float *b2, const float *w3, const float *b3,
                                                    int k0, int n1, int n2, int n3, float *logits, int32_t *pred,
@@ -138,57 +91,176 @@ __global__ __launch_bounds__(256) void mlp3_kernel(const float *x, int64_t M, co
     }
 }
 
-// mlp3_kernel for layer sizes fixed at compile time: every wave requests the weights of all its
-// tiles of all three layers at the start, beside the input rows, so the chain waits for memory
-// once instead of once per layer and weight chunk.
+// The digits networks (K0 -> N1 -> N2 -> N3, K0, N1 and N2 multiples of 64, N3 <= 16) in one
+// launch of 16-row workgroups on v_mfma_f32_16x16x4f32: 1797 rows make 113 workgroups (32-row
+// tiles on 32x32x2 MFMAs made 57, leaving 199 of 256 CUs idle), and a layer's MFMA chain is
+// 16-32 products of 32 cycles instead of 32-64 of 64. Four waves:
+//   layer 1: wave w owns the 16-column tiles w, w + 4, ... of N1; layer 2 the same over N2;
+//   layer 3 (one tile): wave 0;
+// each tile is one MFMA chain over the whole K, lane group g (lanes 16g .. 16g + 15) feeding
+// k = g K/4 + s at step s (the four k of a step are any four, so long as A and B agree), so a
+// lane reads consecutive k: x as float4, the activations as 16-byte LDS reads. Every weight,
+// bias and input a wave needs is requested at the start, before the first product, as
+// unconditional loads from clamped addresses followed by selects (a conditional load becomes a
+// branch whose join waits for it). The activations pass between layers through LDS behind
+// barriers that wait on LDS only. The k order differs from the dense GEMM's, so the logits
+// differ from three dense launches by rounding (each within the float32 error bound of the
+// chain); the argmax follows numpy's rule (first index of the maximum; a NaN wins).
+__device__ __forceinline__ void mlp_lds_barrier() {
+    asm volatile("" ::: "memory");  // no LDS store sinks below the barrier
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitcntLgkm0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int K0, int N1, int N2, int N3>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
-void mlp3_fixed_kernel(const float *x, int64_t M, const float *w1, const float *b1, const float *w2, const float *b2,
-                       const float *w3, const float *b3, float *logits, int32_t *pred, int n_classes) {
-    static_assert(K0 % 2 == 0 && N1 % 2 == 0 && N2 % 2 == 0 && K0 <= MLP_MAXK && N1 <= MLP_MAXK &&
-                      N2 <= MLP_MAXK && N3 <= MLP_MAXK, "even sizes within the LDS tiles");
-    constexpr int P1 = ((N1 + 31) / 32 + 3) / 4, P2 = ((N2 + 31) / 32 + 3) / 4, P3 = ((N3 + 31) / 32 + 3) / 4;
-    __shared__ float buf[2][MLP_ROWS][MLP_PITCH];
-    const int t = threadIdx.x;
-    const int64_t r0 = (int64_t)blockIdx.x * MLP_ROWS;
-    float wr1[P1][K0 / 2], wr2[P2][N1 / 2], wr3[P3][N2 / 2];
-    mlp_load_weights<K0, N1, P1>(w1, wr1);
-    mlp_load_weights<N1, N2, P2>(w2, wr2);
-    mlp_load_weights<N2, N3, P3>(w3, wr3);
+__global__ __launch_bounds__(256) void mlp3_rows16_kernel(const float *x, int64_t M, const float *w1, const float *b1,
+                                                          const float *w2, const float *b2, const float *w3,
+                                                          const float *b3, float *logits, int32_t *pred,
+                                                          int n_classes, PhaseRecord *phase) {
+    static_assert(K0 % 64 == 0 && N1 % 64 == 0 && N2 % 64 == 0 && N3 >= 1 && N3 <= 16 && K0 <= 256 && N1 <= 256 &&
+                      N2 <= 256,
+                  "layer sizes of the 16-row kernel");
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    constexpr int P1 = N1 / 64, P2 = N2 / 64;          // column tiles per wave in layers 1 and 2
+    constexpr int S1 = K0 / 4, S2 = N1 / 4, S3 = N2 / 4;  // MFMA steps of each layer
+    constexpr int H1P = N1 + 4, H2P = N2 + 4;           // LDS row pitches (16-byte rows)
+    __shared__ __align__(16) float h1[16][H1P];
+    __shared__ __align__(16) float h2[16][H2P];
+    __shared__ float lg[16][17];
+    const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+    const int grp = lane >> 4, c16 = lane & 15;
+    const int64_t r0 = (int64_t)blockIdx.x * 16;
+    PITON_PHASE_VARS;
+    PITON_PHASE(0);
+    // the row this lane supplies to layer 1's A operand: a row past M reads row M - 1 instead
+    // (an output row depends on its own input row only, and rows past M are never stored)
+    const int64_t row = r0 + c16 < M ? r0 + c16 : M - 1;
+
+    // -- every operand requested up front, in the order of use (the first products wait for x
+    // and W1 only) --
+    f32x4v xa[S1 / 4];
+    const f32x4v *xp = reinterpret_cast<const f32x4v *>(x + row * K0 + S1 * grp);
 #pragma unroll
-    for (int idx = t; idx < MLP_ROWS * K0; idx += 256) {
-        const int row = idx / K0, kk = idx % K0;
-        const bool ok = r0 + row < M;
-        const float v = x[(ok ? r0 + row : 0) * K0 + kk];
-        buf[0][row][kk] = ok ? v : 0.f;
-    }
-    __syncthreads();
-    mlp_layer_regs<K0, N1, P1>(buf[0], wr1, b1, true, buf[1]);
-    __syncthreads();
-    mlp_layer_regs<N1, N2, P2>(buf[1], wr2, b2, true, buf[0]);
-    __syncthreads();
-    mlp_layer_regs<N2, N3, P3>(buf[0], wr3, b3, false, buf[1]);
-    __syncthreads();
+    for (int q = 0; q < S1 / 4; q++) xa[q] = xp[q];
+    float wb1[P1][S1], wb2[P2][S2], wb3[S3], bias1[P1], bias2[P2];
 #pragma unroll
-    for (int idx = t; idx < MLP_ROWS * N3; idx += 256) {
-        const int row = idx / N3, c = idx % N3;
-        if (r0 + row < M && logits) logits[(r0 + row) * N3 + c] = buf[1][row][c];
+    for (int p = 0; p < P1; p++) {
+        const int col = 16 * (wave + 4 * p) + c16;
+#pragma unroll
+        for (int s = 0; s < S1; s++) wb1[p][s] = w1[(S1 * grp + s) * N1 + col];
+        bias1[p] = (b1 ? b1 : w1)[col];  // a null bias reads a weight, which the epilogue discards
     }
-    if (t < MLP_ROWS && r0 + t < M && pred) {
-        // every logit of the row read first (one LDS round trip), then combined in class order
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < P2; p++) {
+        const int col = 16 * (wave + 4 * p) + c16;
+#pragma unroll
+        for (int s = 0; s < S2; s++) wb2[p][s] = w2[(S2 * grp + s) * N2 + col];
+        bias2[p] = (b2 ? b2 : w2)[col];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // layer 3's operands (used by wave 0 only; loaded by every wave, so no branch waits on them).
+    // Columns past N3 read column N3 - 1: an output column depends on its own weight column
+    // only, and those columns are neither stored nor ranked
+    const bool c3_ok = c16 < N3;
+    const int c3 = c3_ok ? c16 : N3 - 1;
+#pragma unroll
+    for (int s = 0; s < S3; s++) wb3[s] = w3[(S3 * grp + s) * N3 + c3];
+    const float bias3 = (b3 ? b3 : w3)[c3];
+    __builtin_amdgcn_sched_barrier(0);
+    PITON_PHASE_WAIT_LOADS();
+    PITON_PHASE(1);
+
+    // -- layer 1: rows of x times W1 (+ b1, ReLU) into h1 --
+    f32x4v acc1[P1];
+#pragma unroll
+    for (int p = 0; p < P1; p++) acc1[p] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < S1 / 4; q++) {
+        const f32x4v a = xa[q];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int p = 0; p < P1; p++)
+                acc1[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], wb1[p][4 * q + e], acc1[p], 0, 0, 0);
+    }
+    // accumulator r of a tile: row 4 * grp + r, column 16 * tile + c16
+#pragma unroll
+    for (int p = 0; p < P1; p++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float v = acc1[p][r] + (b1 ? bias1[p] : 0.f);
+            if (v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
+            h1[4 * grp + r][16 * (wave + 4 * p) + c16] = v;
+        }
+    mlp_lds_barrier();
+
+    // -- layer 2: h1 W2 (+ b2, ReLU) into h2 --
+    f32x4v acc2[P2];
+#pragma unroll
+    for (int p = 0; p < P2; p++) acc2[p] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < S2 / 4; q++) {
+        const f32x4v a = *reinterpret_cast<const f32x4v *>(&h1[c16][S2 * grp + 4 * q]);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int p = 0; p < P2; p++)
+                acc2[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], wb2[p][4 * q + e], acc2[p], 0, 0, 0);
+    }
+#pragma unroll
+    for (int p = 0; p < P2; p++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float v = acc2[p][r] + (b2 ? bias2[p] : 0.f);
+            if (v < 0.f) v = 0.f;
+            h2[4 * grp + r][16 * (wave + 4 * p) + c16] = v;
+        }
+    mlp_lds_barrier();
+    PITON_PHASE(2);
+    if (wave != 0) {  // wave-uniform; no barrier follows
+        PITON_PHASE(3);
+        PITON_PHASE_END(kPhaseMlp, phase);
+        return;
+    }
+
+    // -- layer 3 (wave 0): h2 W3 + b3, the logits and the argmax of the first n_classes --
+    f32x4v acc3 = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < S3 / 4; q++) {
+        const f32x4v a = *reinterpret_cast<const f32x4v *>(&h2[c16][S3 * grp + 4 * q]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc3 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], wb3[4 * q + e], acc3, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float v = acc3[r] + (b3 ? bias3 : 0.f);
+        const int64_t orow = r0 + 4 * grp + r;
+        if (logits && c3_ok && orow < M) logits[orow * N3 + c16] = v;
+        lg[4 * grp + r][c16] = v;
+    }
+    wave_lds_sync();
+    if (lane < 16 && r0 + lane < M && pred) {
         float lv[N3];
 #pragma unroll
-        for (int c = 0; c < N3; c++) lv[c] = buf[1][t][c];
+        for (int c = 0; c < N3; c++) lv[c] = lg[lane][c];
         float bv = -INFINITY;
         int bi = 0x7FFFFFFF;
 #pragma unroll
         for (int c = 0; c < N3; c++)
             if (c < n_classes) argmax_combine(bv, bi, lv[c], c);
-        pred[r0 + t] = bi;
+        pred[r0 + lane] = bi;
     }
+    PITON_PHASE(3);
+    PITON_PHASE_END(kPhaseMlp, phase);
 }
 
 }  // namespace piton
+
+PITON_PHASE_TU(mlp)
 
 extern "C" int32_t piton_mi355x_mlp3(const float *x, int64_t M, const float *w1, const float *b1, const float *w2,
                                      const float *b2, const float *w3, const float *b3, int64_t k0, int64_t n1,
@@ -209,15 +281,17 @@ extern "C" int32_t piton_mi355x_mlp3(const float *x, int64_t M, const float *w1,
     int rc = require_device();
     if (rc) return rc;
     if (M == 0) return PITON_OK;
-    const int64_t wgs = (M + MLP_ROWS - 1) / MLP_ROWS;
-    PITON_REQUIRE(wgs <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "mlp3: M=%lld too large", (long long)M);
-    // the digits networks (ten logits, or the trained model's sixteen)
-    if (k0 == 64 && n1 == 128 && n2 == 64 && n3 == 10)
-        PITON_LAUNCH((mlp3_fixed_kernel<64, 128, 64, 10>), dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, x,
-                     M, w1, b1, w2, b2, w3, b3, logits, pred, n_classes);
-    else if (k0 == 64 && n1 == 128 && n2 == 64 && n3 == 16)
-        PITON_LAUNCH((mlp3_fixed_kernel<64, 128, 64, 16>), dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, x,
-                     M, w1, b1, w2, b2, w3, b3, logits, pred, n_classes);
+    const int64_t wgs = (M + MLP_ROWS - 1) / MLP_ROWS, wgs16 = (M + 15) / 16;
+    PITON_REQUIRE(wgs16 <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "mlp3: M=%lld too large", (long long)M);
+    // the digits networks (ten logits, or the trained model's sixteen) with 16-byte aligned
+    // input rows: 16-row tiles; other sizes: 32-row tiles, the dense GEMM's bits
+    const bool digits = k0 == 64 && n1 == 128 && n2 == 64 && (n3 == 10 || n3 == 16) && aligned16(x);
+    if (digits && n3 == 10)
+        PITON_LAUNCH((mlp3_rows16_kernel<64, 128, 64, 10>), dim3((unsigned)wgs16), dim3(256), 0, (hipStream_t)stream,
+                     x, M, w1, b1, w2, b2, w3, b3, logits, pred, n_classes, phase_slot());
+    else if (digits)
+        PITON_LAUNCH((mlp3_rows16_kernel<64, 128, 64, 16>), dim3((unsigned)wgs16), dim3(256), 0, (hipStream_t)stream,
+                     x, M, w1, b1, w2, b2, w3, b3, logits, pred, n_classes, phase_slot());
     else
         PITON_LAUNCH(mlp3_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, x, M, w1, b1, w2, b2, w3,
                      b3, (int)k0, (int)n1, (int)n2, (int)n3, logits, pred, n_classes);

@@ -18,8 +18,11 @@
 //     input row and the chunk is whole, scalar stores at the row's two ends;
 //   * exp is v_exp_f32 on (x - max) * log2(e): about 1e-7 relative on the entries that carry
 //     the row's weight; the row sum's reciprocal is correctly rounded;
-//   * special values follow IEEE/numpy: a +inf or NaN entry, or an all -inf row, makes the
-//     whole row NaN; a -inf entry in a finite row gives exactly 0;
+//   * special values: a +inf or +NaN entry, or an all -inf row, makes the whole row NaN, as
+//     in numpy and in the QPU emulator; a -inf entry in a finite row gives exactly 0; a -NaN
+//     entry gives exactly 0 and the rest of the row is a normal softmax, as in the emulator,
+//     whose fmax orders -NaN lowest and whose float ALUs read it as -inf
+//     (piton/qpu/emulator.py:139-147, 173-177, 201-205, 224-225); numpy makes that row NaN;
 //   * longer rows take a workgroup-per-row kernel that reads the row three times (max, sum,
 //     write).
 #include "common.h"
@@ -54,6 +57,13 @@ namespace piton {
 __device__ __forceinline__ float exp_row(float d) {
     const float kL2E = 1.44269502162933349609375f;  // float(log2 e)
     return __builtin_amdgcn_exp2f(d * kL2E);
+}
+
+// The emulator's view of an operand for the row maximum and the subtraction: a NaN with the
+// sign bit set (bits above 0xFF800000) is -inf; every other value is itself (a +NaN stays NaN,
+// so the row still comes out NaN). Two VALU operations per element of an HBM-bound kernel.
+__device__ __forceinline__ float qpu_neg_nan(float x) {
+    return __float_as_uint(x) > 0xFF800000u ? -INFINITY : x;
 }
 
 // Loads row r's aligned float4 window into b: T threads share the row, thread t holding
@@ -112,6 +122,8 @@ __device__ __forceinline__ void softmax_store_row(float *out, int64_t out_rs, in
             for (int j = 0; j < 4; j++)
                 if (!(e0 + j >= 0 && e0 + j < n)) b[c][j] = -INFINITY;
         }
+#pragma unroll
+        for (int j = 0; j < 4; j++) b[c][j] = qpu_neg_nan(b[c][j]);
         mx = fmaxf(mx, fmaxf(fmaxf(b[c].x, b[c].y), fmaxf(b[c].z, b[c].w)));
     }
     const float m = row_reduce<T>(mx, MaxOp(), red);
@@ -236,13 +248,13 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(float *out, const flo
     const float *rp = in + row * in_rs;
     float *op = out + row * out_rs;
     float mx = -INFINITY;
-    for (int64_t i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, rp[i]);
+    for (int64_t i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, qpu_neg_nan(rp[i]));
     const float m = block_reduce(mx, red, true);
     float s = 0.f;
-    for (int64_t i = threadIdx.x; i < n; i += 256) s += exp_row(rp[i] - m);
+    for (int64_t i = threadIdx.x; i < n; i += 256) s += exp_row(qpu_neg_nan(rp[i]) - m);
     s = block_reduce(s, red, false);
     const float inv = 1.0f / s;
-    for (int64_t i = threadIdx.x; i < n; i += 256) op[i] = exp_row(rp[i] - m) * inv;
+    for (int64_t i = threadIdx.x; i < n; i += 256) op[i] = exp_row(qpu_neg_nan(rp[i]) - m) * inv;
 }
 
 // Launches the wave-per-row kernel: one row per wave (mode 0), or persistent waves, as many

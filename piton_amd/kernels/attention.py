@@ -48,10 +48,16 @@ def attention_flops(n_ctx, head_dim, causal=False, heads=1) -> float:
     return 4.0 * n_ctx * n_ctx * head_dim * heads * (0.5 if causal else 1.0)
 
 
-def run_attention(q, k, v, causal=False, block_m=64, block_n=32, k_layout="nd", sm_scale=None):
+def run_attention(q, k, v, causal=False, block_m=64, block_n=32, compiled=None, k_layout="nd", sm_scale=None):
     """attn_fwd_kernel on [N, D] or [H, N, D] float32 q, k, v (numpy or GPU tensors); k_layout
-    "dn" passes K pre-transposed ([H, D, N]). Returns out (the type of q). The MI355X
-    counterpart of examples/attention.py:200-222."""
+    "dn" passes K pre-transposed ([H, D, N]). Returns (out, record, stats) as
+    examples/attention.py:200-222 returns (out, compiled kernel, emulator stats): `out` has the
+    type of q, `record` is the launch's LaunchRecord (the kernel's name, grid, entry, signature
+    and constants) and `stats` its `last_stats` (the device kernels run with their grids,
+    registers and spills, and the launch's FLOPs and bytes). `compiled` is accepted for the
+    reference's signature and unused: the device library is built ahead of time, so there is
+    no per-shape compile to reuse."""
+    del compiled
     import torch
     is_np = isinstance(q, np.ndarray)
     tq, tk, tv = (torch.as_tensor(np.ascontiguousarray(t, np.float32)) if is_np else t for t in (q, k, v))
@@ -70,14 +76,15 @@ def run_attention(q, k, v, causal=False, block_m=64, block_n=32, k_layout="nd", 
     st = contiguous_strides(head_dim, k_layout, n_ctx)
     scale = float(1.0 / np.sqrt(head_dim)) if sm_scale is None else float(sm_scale)
     grid = (cdiv(n_ctx, block_m), heads)
-    attn_fwd_kernel[grid](tq, tk, tv, out, scale,
-                          n_ctx * head_dim, st["stride_qm"], n_ctx * head_dim, st["stride_kn"], st["stride_kk"],
-                          n_ctx * head_dim, st["stride_vn"], n_ctx * head_dim, st["stride_om"], n_ctx,
-                          HEAD_DIM=head_dim, BLOCK_M=block_m, BLOCK_N=block_n, CAUSAL=bool(causal),
-                          EVEN_N=n_ctx % block_n == 0, device="mi355x")
+    record = attn_fwd_kernel[grid](tq, tk, tv, out, scale,
+                                   n_ctx * head_dim, st["stride_qm"], n_ctx * head_dim, st["stride_kn"],
+                                   st["stride_kk"], n_ctx * head_dim, st["stride_vn"], n_ctx * head_dim,
+                                   st["stride_om"], n_ctx,
+                                   HEAD_DIM=head_dim, BLOCK_M=block_m, BLOCK_N=block_n, CAUSAL=bool(causal),
+                                   EVEN_N=n_ctx % block_n == 0, device="mi355x")
     if squeeze:
         out = out[0]
     if is_np:
         torch.cuda.current_stream().synchronize()
-        return out.cpu().numpy()
-    return out
+        out = out.cpu().numpy()
+    return out, record, record.last_stats

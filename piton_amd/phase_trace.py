@@ -1,5 +1,5 @@
 """Launch phases of the HBM-bound softmax, the one-generation attention kernel, the decode
-attention of the KV-cached decoder and its fused decode step (diagnostics).
+attention of the KV-cached decoder, its fused decode step and the digits MLP (diagnostics).
 
 `python -m piton_amd.phase_trace` builds a traced copy of the library beside the product one
 (-DPITON_PHASE_TRACE: every traced wave keeps s_memrealtime stamps -- a 100 MHz clock shared by
@@ -170,6 +170,33 @@ def decode_layer_phases(n_keys: int, batch: int = 64, heads: int = 4, d_head: in
     return {key: statistics.median(r[key] for r in rows) * TICK_US for key in rows[0]}
 
 
+def mlp_phases(batch: int, launches: int = 12):
+    """The digits MLP in one launch (piton_mi355x_mlp3, 16 rows per workgroup): per launch,
+    medians over waves of the wait for every operand (x, the three layers' weights and biases),
+    of layers 1 and 2 to the barrier after layer 2, and of wave 0's layer 3, logits and argmax."""
+    import numpy as np
+    import torch
+
+    from . import digits
+    from .runtime import mi355x as rt
+    layers = digits.he_normal_mlp(seed=1729)
+    mlp = digits.MLP(layers, max_batch=batch)
+    x = torch.from_numpy(np.random.default_rng(0).integers(0, 17, (batch, 64)).astype(np.float32)).cuda()
+    per = _trace("mlp", lambda i: mlp.run(x), launches)
+    rows = []
+    for k in range(1, len(per) - 1):
+        ls = per[k]
+        t0 = min(r[0] for r in ls)
+        w0 = [r for r in ls if (r[4] >> 32) % 4 == 0]
+        rows.append(dict(waves=len(ls), last_wave_start=max(r[0] for r in ls) - t0,
+                         operands=statistics.median(r[1] - r[0] for r in ls),
+                         layers12=statistics.median(r[2] - r[1] for r in ls),
+                         layer3=statistics.median(r[3] - r[2] for r in w0),
+                         end=max(r[3] for r in ls) - t0,
+                         gap_to_next=min(r[0] for r in per[k + 1]) - max(r[3] for r in ls)))
+    return {key: statistics.median(r[key] for r in rows) * (1 if key == "waves" else TICK_US) for key in rows[0]}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--no-build", action="store_true", help="use the traced library already built")
@@ -205,6 +232,14 @@ def main():
         m = decode_layer_phases(nk)
         print(f"| {nk} keys | {us(m['layernorm'])} | {us(m['projection'])} | {us(m['cache_copies'])} | "
               f"{us(m['attention'])} | {us(m['end'])} | {us(m['gap_to_next'])} |")
+    print()
+    print("| digits MLP, one launch | waves | last wave starts | every operand in | layers 1 and 2 | "
+          "layer 3 and argmax (wave 0) | last wave ends | gap to next launch |")
+    print("|---|---|---|---|---|---|---|---|")
+    for b in (1, 256, 1797):
+        m = mlp_phases(b)
+        print(f"| batch {b} | {int(m['waves'])} | {us(m['last_wave_start'])} | {us(m['operands'])} | "
+              f"{us(m['layers12'])} | {us(m['layer3'])} | {us(m['end'])} | {us(m['gap_to_next'])} |")
 
 
 if __name__ == "__main__":

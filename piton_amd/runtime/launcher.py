@@ -168,9 +168,10 @@ def run_mi355x(jitfn, grid, signature, constants, values) -> LaunchRecord:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
     getattr(rt, entry)(*resolved)
+    if timed:
+        e1.record()  # right behind the launch: the host work below is not in the interval
     stats = {"launches": rt.last_launches(), **lookup(jitfn).work(_env(grid, constants, values))}
     if timed:
-        e1.record()
         e1.synchronize()
         stats["elapsed_us"] = e0.elapsed_time(e1) * 1e3
     if staged:

@@ -110,6 +110,9 @@ class TinyGPT:
     def _forward(self, p0: int, p1: int):
         cfg, B = self.cfg, self.B
         D, F, H, Dh, V = cfg.d_model, cfg.d_mlp, cfg.n_heads, cfg.head_dim, cfg.vocab
+        if p0 > 0 and p1 != p0 + 1:
+            # checked before any launch: nothing is embedded or written into the caches
+            raise ValueError("decode steps take one position at a time")
         n = (p1 - p0) * B
         r0 = p0 * B
         x, h, att, mlp = (t[r0:r0 + n] for t in (self.x, self.h, self.att, self.mlp))
@@ -144,8 +147,6 @@ class TinyGPT:
                                     3 * D, Dh, B * 3 * D, 3 * D, Dh, B * 3 * D, 1, 3 * D, Dh, B * 3 * D,
                                     D, Dh, B * D, p1, B, H, Dh, True)
             else:
-                if p1 != p0 + 1:
-                    raise ValueError("decode steps take one position at a time")
                 if not fused_step:
                     rt.attn_decode(qkv, cache[:, D:], cache[:, 2 * D:], att, scale, 3 * D, Dh, 3 * D, Dh,
                                    B * 3 * D, 3 * D, Dh, B * 3 * D, D, Dh, p1, B, H, Dh)

@@ -21,6 +21,10 @@ emulator and writes their inputs and outputs to tests/golden/emulator/*.npz:
                 (`--full-mlp`, about half an hour of emulation)
   layernorm.npz row layernorm (the kernel of tests/test_reroll_reduce.py:199-208) at BLOCK 256
                 and 128, and add_kernel's x + y (`--layernorm`)
+  softmax_specials.npz  softmax_kernel (BLOCK 256) over rows of special values: NaN, -NaN,
+                +inf, -inf, -0, +0 and denormals in the first register, alone and mixed with
+                N(0, 1) entries (the pattern of tests/test_reroll_reduce.py:157-174, plus rows
+                with only a -NaN entry) (`--softmax-specials`)
   softmax_long.npz  softmax_kernel rows at BLOCK_SIZE 1024 and 2048 (n_cols 1000, 1023, 1823),
                 which compile only with the reduction reroll of piton/reroll.py switched on
                 (PITON_REROLL_REDUCE=1, the build of tests/test_reroll_reduce.py:37-44)
@@ -253,6 +257,33 @@ def softmax_long_vectors(rng):
     return out
 
 
+def softmax_specials_vectors(rng):
+    """softmax_kernel at BLOCK 256 on 12 rows of 256: the special-value rows of
+    tests/test_reroll_reduce.py:157-174 and four rows whose only special entry is a -NaN (first,
+    middle, last column; two of them)."""
+    import kernels as K
+    rows, block = 12, 256
+    neg_nan = np.array([0xFFC00000], np.uint32).view(np.float32)[0]
+    x = rng.standard_normal((rows, block)).astype(np.float32)
+    x[0, :8] = np.array([np.nan, neg_nan, np.inf, -np.inf, -0.0, 0.0, 1e-40, -1e-40], np.float32)
+    x[1, 3] = np.inf
+    x[2, 0] = -np.inf
+    x[3, :] = -0.0
+    x[4, 0] = 1e-40
+    x[4, 17] = -1e-40
+    x[5, 16] = np.nan
+    x[6, :] = -np.inf
+    x[7, 255] = np.nan
+    x[8, 0] = neg_nan
+    x[9, 130] = neg_nan
+    x[10, 255] = neg_nan
+    x[11, 40] = neg_nan
+    x[11, 41] = neg_nan
+    y = np.full((rows, block), np.float32(-7.0))
+    K.softmax_kernel[(rows,)](y, x, block, block, block, BLOCK_SIZE=block)
+    return {"x": x, "y": y, "shape": np.array([rows, block, block, block], np.int64)}
+
+
 def layernorm_vectors(rng):
     """Row layernorm without affine (the kernel of tests/test_reroll_reduce.py:199-208) over 3 rows
     at (BLOCK, n) = (256, 256), (256, 200), (128, 100), (128, 127), built the way that test builds
@@ -296,6 +327,12 @@ def main():
         t0 = time.time()
         np.savez_compressed(os.path.join(OUT, "softmax_long.npz"), **softmax_long_vectors(np.random.default_rng(7)))
         print(f"softmax_long: {time.time() - t0:.1f} s", flush=True)
+        return
+    if "--softmax-specials" in sys.argv:
+        t0 = time.time()
+        np.savez_compressed(os.path.join(OUT, "softmax_specials.npz"),
+                            **softmax_specials_vectors(np.random.default_rng(13)))
+        print(f"softmax_specials: {time.time() - t0:.1f} s", flush=True)
         return
     if "--layernorm" in sys.argv:
         t0 = time.time()

@@ -127,17 +127,52 @@ def test_ragged_batches_reuse_buffers():
 
 
 @pytest.mark.parametrize("m,sizes", [(1797, (64, 128, 64, 10)), (1797, (64, 128, 64, 16)), (33, (64, 128, 64, 10)),
-                                     (1, (64, 128, 64, 10)), (70, (32, 256, 96, 40))])
-def test_one_launch_chain_equals_three_dense_launches(m, sizes):
-    """mlp3 (the whole chain in one launch) gives the three dense launches' logits and
-    predictions bit for bit: same MFMA chains in the same k order, same epilogues."""
+                                     (1, (64, 128, 64, 10)), (16, (64, 128, 64, 16)), (70, (32, 256, 96, 40))])
+def test_one_launch_chain_against_three_dense_launches(m, sizes):
+    """mlp3 (the whole chain in one launch) against the three dense launches. The digits sizes
+    run 16-row tiles on 16x16x4 MFMAs, whose k order differs from the dense GEMM's: both chains'
+    logits lie within the float32 error bounds of the float64 chain, they agree to 2e-6 relative,
+    and their predictions agree wherever the bounds certify the top logit. Other sizes run the
+    dense GEMM's MFMA chains in its k order: the same logits and predictions bit for bit."""
     layers = digits.he_normal_mlp(seed=m + sizes[-1], sizes=sizes)
     layers = [(w, np.random.default_rng(i).normal(0, 0.1, b.shape).astype(np.float32)) for i, (w, b) in enumerate(layers)]
-    mlp = digits.MLP(layers, max_batch=m, n_classes=min(10, sizes[-1]))
-    x = torch.from_numpy(np.random.default_rng(m).integers(0, 17, (m, sizes[0])).astype(np.float32)).cuda()
+    n_classes = min(10, sizes[-1])
+    mlp = digits.MLP(layers, max_batch=m, n_classes=n_classes)
+    xh = np.random.default_rng(m).integers(0, 17, (m, sizes[0])).astype(np.float32)
+    x = torch.from_numpy(xh).cuda()
     lf, pf = (t.clone() for t in mlp.run(x, fused=True))
+    (launch,) = rt.last_launches()
     ll, pl = (t.clone() for t in mlp.run(x, fused=False))
     torch.cuda.synchronize()
+    lf, ll, pf, pl = lf.cpu().numpy(), ll.cpu().numpy(), pf.cpu().numpy(), pl.cpu().numpy()
+    assert launch["scratch_bytes"] == 0
+    if sizes[:3] == (64, 128, 64):
+        assert launch["kernel"].startswith("mlp3_rows16_kernel") and launch["grid"][0] == -(-m // 16), launch
+        chain = [(w, b, i < 2) for i, (w, b) in enumerate(layers)]
+        ref, bound = fp64.mlp_with_bounds(xh, chain, unit=2.0 ** -23)
+        assert (np.abs(lf - ref) <= bound).all() and (np.abs(ll - ref) <= bound).all()
+        assert fp64.rel_fro(lf, ll) <= 2e-6
+        _, certified = fp64.certified_argmax(ref, 2 * bound, n_classes)
+        np.testing.assert_array_equal(pf[certified], pl[certified])
+        np.testing.assert_array_equal(pf, oracle.argmax_rows(lf, n_classes))
+    else:
+        assert launch["kernel"] == "mlp3_kernel", launch
+        np.testing.assert_array_equal(lf, ll)
+        np.testing.assert_array_equal(pf, pl)
+
+
+def test_one_launch_chain_unaligned_input_takes_the_general_kernel():
+    """Digits input rows that are not 16-byte aligned take the 32-row kernel, whose logits equal
+    the dense launches' bit for bit."""
+    layers = digits.he_normal_mlp(seed=5)
+    mlp = digits.MLP(layers, max_batch=40)
+    xh = np.random.default_rng(5).integers(0, 17, (40 * 64 + 1,)).astype(np.float32)
+    x = torch.from_numpy(xh).cuda()[1:].view(40, 64)
+    lf, pf = (t.clone() for t in mlp.run(x, fused=True))
+    (launch,) = rt.last_launches()
+    ll, pl = (t.clone() for t in mlp.run(x, fused=False))
+    torch.cuda.synchronize()
+    assert launch["kernel"] == "mlp3_kernel", launch
     np.testing.assert_array_equal(lf.cpu().numpy(), ll.cpu().numpy())
     np.testing.assert_array_equal(pf.cpu().numpy(), pl.cpu().numpy())
 

@@ -2,7 +2,10 @@
 
 Bar: relative Frobenius error <= 1e-5 vs float64 over finite rows and no larger than the
 oracle's (the emulator's arithmetic); the NaN pattern of rows with special values matches
-numpy's; columns past min(n_cols, BLOCK_SIZE) are never written."""
+numpy's, except that a -NaN entry is 0 and leaves its row finite, as in the emulator; columns
+past min(n_cols, BLOCK_SIZE) are never written."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -15,6 +18,7 @@ from piton_amd.runtime import mi355x as rt
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "emulator")
 
 
 def run(x, n_cols=None, block=None, out=None):
@@ -70,6 +74,55 @@ def test_benchmark_shapes_with_special_rows(n):
     emu = oracle.softmax(x[sample], n)
     ref = fp64.softmax(x[sample])
     assert fp64.rel_fro(got[sample], ref) <= fp64.rel_fro(emu, ref)
+
+
+NEG_NAN = np.array([0xFFC00000], np.uint32).view(np.float32)[0]
+
+
+def neg_nan_as_ninf(x):
+    """The emulator's reading of a -NaN operand (piton/qpu/emulator.py:173-177, 201-205): -inf."""
+    x = np.array(x, np.float32)
+    x[np.isnan(x) & np.signbit(x)] = -np.inf
+    return x
+
+
+def test_special_value_rows_match_the_emulator():
+    """The emulator's own output on NaN, -NaN, +inf, -inf, -0, +0 and denormal rows
+    (tests/test_reroll_reduce.py:157-174; fixture written by the reference's emulator): the same
+    NaN pattern, exact zeros where it has them, and finite rows within the tolerance of float64
+    applied to the emulator's reading of the operands and no worse than the emulator there."""
+    s = np.load(os.path.join(GOLDEN, "softmax_specials.npz"))
+    x, want = s["x"], s["y"]
+    rows, cols = x.shape
+    got = run(torch.from_numpy(x).cuda(), cols, cols).cpu().numpy()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    np.testing.assert_array_equal(got == 0, want == 0)
+    fin = np.isfinite(want).all(axis=1)
+    ref = fp64.softmax(neg_nan_as_ninf(x[fin]))
+    assert fp64.rel_fro(got[fin], ref) <= max(fp64.rel_fro(want[fin], ref), 1e-7)
+
+
+@pytest.mark.parametrize("n", [1024, 4096, 1823, 2048, 6001, 20000])
+def test_negative_nan_entries(n):
+    """A -NaN entry is exactly 0 and the rest of its row a normal softmax, in every row kernel
+    (one wave per row, persistent waves, one workgroup per row, three passes), as in the
+    oracle; a +NaN entry still makes its row NaN."""
+    rng = np.random.default_rng(n + 5)
+    x = (rng.standard_normal((6, n)) * 4).astype(np.float32)
+    x[0, 0] = NEG_NAN
+    x[1, n - 1] = NEG_NAN
+    x[2, n // 3] = NEG_NAN
+    x[2, n // 2] = NEG_NAN
+    x[3, 7] = NEG_NAN
+    x[3, 8] = np.nan
+    got = run(torch.from_numpy(x).cuda()).cpu().numpy()
+    assert got[0, 0] == 0 and got[1, n - 1] == 0 and got[2, n // 3] == 0 and got[2, n // 2] == 0
+    assert np.isnan(got[3]).all() and not np.isnan(got[[0, 1, 2, 4, 5]]).any()
+    ref = fp64.softmax(neg_nan_as_ninf(x[:3]))
+    assert fp64.rel_fro(got[:3], ref) <= TOL
+    emu = np.asarray(oracle.softmax(x[:3], n))
+    np.testing.assert_array_equal(emu == 0, got[:3] == 0)
+    assert fp64.rel_fro(got[:3], ref) <= max(fp64.rel_fro(emu, ref), 1e-7)
 
 
 def test_block_smaller_than_row_and_untouched_columns():

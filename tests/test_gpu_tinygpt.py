@@ -3,10 +3,10 @@
 
 The reference has no decoder, so parity is against the build's own float64 model, which is
 pinned by invariants and by hand-set weights with a closed-form token (tests/tinygpt_cases.py).
-Bar: every piece within float32 tolerance of float64; at the config the greedy token ids equal
-the float64 model's on all 64 sequences; on the smaller seeded cases a sequence may diverge only
-at a step whose float64 top-2 logit margin is below TAU (a near-tie that float32 cannot
-resolve), reported with its margin."""
+Bar: every piece within float32 tolerance of float64; a sequence's greedy token ids equal the
+float64 model's, except that a sequence may diverge at a step whose float64 top-2 logit margin
+is below TAU (a near-tie that float32 cannot resolve), reported with its margin; at the config
+at most MAX_TIES of the 64 sequences may (today none does)."""
 import numpy as np
 import pytest
 import torch
@@ -18,6 +18,7 @@ from piton_amd.runtime import mi355x as rt
 
 pytestmark = pytest.mark.gpu
 TAU = 1e-4  # float32 logits of this model carry ~1e-6 absolute error; margins below TAU are ties
+MAX_TIES = 2  # sequences of the 64 x 128 config that may leave the float64 path at a near-tie
 
 
 def test_linear_residual_relu_strided():
@@ -244,7 +245,10 @@ def test_decode_layer_matches_float64_and_the_two_launches(B, H, n_keys, pad):
     ldo = Dm + 2 * pad
     out = torch.full((B, ldo), -5.0, device="cuda")
     rt.decode_layer(tx, Dm + 4 * pad, 1e-5, tw, tb, tc, ldc, out, ldo, 1 / 8, n_keys, B, H, 64, Dm)
+    launches = rt.last_launches()
     torch.cuda.synchronize()
+    # one workgroup of 512 threads per (sequence, head), and no register spills
+    assert [(x["grid"][0], x["block"][0], x["scratch_bytes"]) for x in launches] == [(B * H, 512, 0)], launches
     got_c, got = tc.cpu().numpy(), out.cpu().numpy()
     new = slice((n_keys - 1) * B, n_keys * B)
     assert fp64.rel_fro(got_c[new, :3 * Dm], y_ref) <= 2e-6
@@ -338,7 +342,10 @@ def test_lm_head_argmax_matches_float64_and_the_two_launches(M, N, K, n_classes,
     logits = torch.full((M, N + 3), -7.0, device="cuda")
     nxt = torch.full((M,), -1, dtype=torch.int32, device="cuda")
     rt.lm_head_argmax(tx, K + 4, 1e-5, tw, tb, logits, N + 3, nxt, M, N, K, n_classes)
+    launches = rt.last_launches()
     torch.cuda.synchronize()
+    # one workgroup of 512 threads per row, and no register spills
+    assert [(x["grid"][0], x["block"][0], x["scratch_bytes"]) for x in launches] == [(M, 512, 0)], launches
     got, tok = logits.cpu().numpy(), nxt.cpu().numpy()
     ref = tinygpt64.layernorm(x[:, :K].astype(np.float64), 1e-5) @ w + (0 if b is None else b)
     ok = np.isfinite(ref).all(axis=1)
@@ -380,7 +387,28 @@ def test_fused_and_unfused_decode_give_the_same_tokens():
     for got in (fused, plain):
         for seq, pos, margin in tinygpt64.first_divergence(got, want, margins, 32):
             assert margin < TAU, (seq, pos, margin)
-    np.testing.assert_array_equal(fused, plain)
+    # the two paths round differently (dot products against matrix-core products), so each
+    # sequence is compared up to its first near-tie step of the float64 decode
+    for b in range(16):
+        ties = np.flatnonzero(margins[b] < TAU)
+        end = 32 + (int(ties[0]) if ties.size else 40)
+        np.testing.assert_array_equal(fused[b, :end], plain[b, :end])
+
+
+def test_decode_step_of_two_positions_is_refused_before_any_launch():
+    """A decode step (p0 > 0) must cover one position: the call raises before it embeds a token
+    or writes a cache row, on the fused path and the unfused one."""
+    w = tinygpt.init_weights(seed=0)
+    for fused in (True, False):
+        model = tinygpt.TinyGPT(w, batch=4, fused_decode=fused)
+        model.generate(tinygpt.seeded_prompts(batch=4, length=8, seed=1), 2, graph=False)
+        torch.cuda.synchronize()
+        before = [t.clone() for t in (model.x, *model.qkv)]
+        with pytest.raises(ValueError, match="one position at a time"):
+            model._forward(8, 10)
+        torch.cuda.synchronize()
+        for a, b in zip(before, (model.x, *model.qkv)):
+            assert torch.equal(a.isnan(), b.isnan()) and torch.equal(a.nan_to_num(), b.nan_to_num())
 
 
 def test_strided_embedding_and_bad_ids():
@@ -446,9 +474,12 @@ def test_config_greedy_64x128_matches_float64():
     got = model.generate(prompts, 128)
     want, margins = tinygpt64.generate(w, prompts, 128)
     div = tinygpt64.first_divergence(got, want, margins, 32)
-    # every sequence's 160 token ids equal the float64 model's: no divergence is allowed, and one
-    # would be reported with its float64 top-2 margin
-    assert div == [], f"token ids differ in {len(div)} of 64 sequences (seq, pos, fp64 margin): {div}"
+    # the float64 decode passes steps whose top-2 margin is as small as 1.4e-5 (below TAU), where
+    # float32 rounding may pick the other token: a sequence may leave the float64 path only at
+    # such a near-tie, and at most MAX_TIES of the 64 may (none do at this seed; the benchmark
+    # reports the count). Any divergence at a resolved step fails.
+    assert all(margin < TAU for _, _, margin in div), f"divergence at a resolved step (seq, pos, margin): {div}"
+    assert len(div) <= MAX_TIES, f"token ids differ in {len(div)} of 64 sequences (seq, pos, fp64 margin): {div}"
 
 
 def test_graph_replays_equal_eager_decoding():

@@ -73,6 +73,18 @@ def test_softmax_rows(i):
     assert (want[:, cols:] == np.float32(-7.0)).all()  # the kernel leaves the rest of the row
 
 
+def test_softmax_special_value_rows():
+    """NaN, -NaN, +inf, -inf, -0, +0 and denormal entries (tests/test_reroll_reduce.py:157-174)
+    and rows whose only special entry is a -NaN: the emulator makes a -NaN entry exactly 0 and
+    the rest of its row a normal softmax (fmax orders -NaN lowest, the ALUs read it as -inf)."""
+    s = load("softmax_specials")
+    rows, cols, block, _ = (int(v) for v in s["shape"])
+    x, want = s["x"], s["y"]
+    assert_bits(np.asarray(oracle.softmax(x, cols, block)), want)
+    assert np.isnan(want[[0, 1, 5, 6, 7]]).all() and np.isfinite(want[[2, 3, 4, 8, 9, 10, 11]]).all()
+    assert want[8, 0] == 0 and want[9, 130] == 0 and want[10, 255] == 0 and (want[11, 40:42] == 0).all()
+
+
 @pytest.mark.parametrize("i", range(3))
 def test_softmax_long_rows(i):
     """BLOCK_SIZE 1024 (n_cols 1000, 1023) and 2048 (n_cols 1823, the config's non-power-of-two

@@ -30,6 +30,13 @@ int check_launch(const char *what);
 // require_device(), which every entry calls before its first launch).
 void note_launch(const void *fn, const char *name, dim3 grid, dim3 block, uint32_t dyn_lds);
 void reset_launches();
+// the same with the kernel's recorded name given (a template's parameter values)
+#define PITON_LAUNCH_NAMED(kernel, name, grid, block, lds, stream, ...)                                       \
+    do {                                                                                                      \
+        ::piton::note_launch(reinterpret_cast<const void *>(&kernel), (name), dim3(grid), dim3(block),        \
+                             (uint32_t)(lds));                                                                \
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                                   \
+    } while (0)
 #define PITON_LAUNCH(kernel, grid, block, lds, stream, ...)                                                   \
     do {                                                                                                      \
         ::piton::note_launch(reinterpret_cast<const void *>(&kernel), #kernel, dim3(grid), dim3(block),       \
@@ -94,7 +101,7 @@ static inline PhaseRecord *phase_slot() { return nullptr; }
 #endif
 // kernel ids of the trace records
 constexpr uint32_t kPhaseSoftmaxRows = 1, kPhaseSoftmaxWg = 2, kPhaseAttnFast = 3, kPhaseAttnDecodeShort = 4,
-                   kPhaseDecodeLayer = 5, kPhaseMlp = 6;
+                   kPhaseDecodeLayer = 5, kPhaseMlp = 6, kPhaseGemmSplit = 7;
 
 // numpy's argmax rule on (value, index) pairs: a NaN beats any number, the larger value beats
 // the smaller, equal values and two NaNs go to the lower index. The combine is associative and
@@ -106,6 +113,15 @@ __device__ __forceinline__ void argmax_combine(float &v, int &i, float v2, int i
         v = v2;
         i = i2;
     }
+}
+
+// Holds a kernel argument in a scalar register from this point on. Without it the compiler may
+// load an argument from the kernarg segment where it is first used, and a load late in a short
+// kernel is one more memory round trip on its critical path.
+template <class T>
+__device__ __forceinline__ T sgpr_keep(T v) {
+    asm volatile("" : "+s"(v));
+    return v;
 }
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -18,6 +18,7 @@
 //     so the stored elements equal sum_k A[m,k] B[k,n] exactly as the reference's masks give;
 //   * tile order: workgroups renumbered so each XCD gets a contiguous run of logical ids,
 //     then the reference's GROUP_SIZE_M grouping (kernels.py:28-36) on those ids.
+#include <string>
 #include <type_traits>
 
 #include "common.h"
@@ -46,7 +47,21 @@ struct GemmArgs {
     int a_kfast, b_nfast;  // scalar loaders: which index runs fastest across threads
     float ln_eps;          // small-row kernel with LN: rows of A are layer-normalised first
     int tile0;             // register-direct kernel: the logical id of the launch's first tile
+    PhaseRecord *phase;    // split kernel: the launch's phase-trace records (diagnostics builds; null otherwise)
 };
+
+// Holds the epilogue's arguments (C and its strides, bias, ReLU, residual) in scalar registers
+// from the kernel's start: otherwise the compiler reloads them from the kernarg segment at the
+// epilogue, one more memory round trip at the end of every launch.
+__device__ __forceinline__ void keep_epilogue_args(GemmArgs &g) {
+    g.c = sgpr_keep(g.c);
+    g.s_cm = sgpr_keep(g.s_cm);
+    g.s_cn = sgpr_keep(g.s_cn);
+    g.bias = sgpr_keep(g.bias);
+    g.relu = sgpr_keep(g.relu);
+    g.res = sgpr_keep(g.res);
+    g.s_rm = sgpr_keep(g.s_rm);
+}
 
 // Loads the A tile (GBM x GBK at m0, k0) into 16 registers per thread.
 // A_L == VEC_ROW: k contiguous; VEC_COL: m contiguous; SCALAR: any strides.
@@ -202,6 +217,7 @@ template <int A_L, int B_L, bool FULL>
 __global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(
     kStages == 1 ? (FULL ? 4 : (A_L == SCALAR || B_L == SCALAR) ? 2 : 3) : 1)))
 void gemm_f32_kernel(GemmArgs g) {
+    keep_epilogue_args(g);
     constexpr int SB = (B_L == VEC_ROW) ? kStrideB : kStrideBT;
     __shared__ float As[kStages][GBK][kStrideAT];
     __shared__ float Bs[kStages][GBK][SB];
@@ -367,6 +383,7 @@ template <bool ONE_GEN, bool AKC, bool BKC, int NBW>
 __global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(
     ONE_GEN ? (NBW > DNB ? 1 : PITON_GEMM_ONE_GEN_WAVES) : PITON_GEMM_DIRECT_WAVES)))
 void gemm_direct_kernel(GemmArgs g) {
+    keep_epilogue_args(g);
     static_assert(ONE_GEN || NBW == DNB, "the wide form runs one workgroup per CU");
     constexpr int WNB = NBW, WBN = 64 * NBW;  // blocks per wave along N, workgroup tile columns
     const int t = threadIdx.x;
@@ -526,6 +543,10 @@ void gemm_direct_kernel(GemmArgs g) {
 #ifndef PITON_SPLIT_WAVES_PER_CU
 #define PITON_SPLIT_WAVES_PER_CU 8
 #endif
+// the wide 64 x 128 tile of the split kernel (0: square tiles only)
+#ifndef PITON_SPLIT_WIDE
+#define PITON_SPLIT_WIDE 1
+#endif
 // the direct kernel takes whole-tile shapes with at least this many 128 x 128 tiles per CU
 // grids with more tiles than CUs run as one launch per generation of one tile per CU (0: one
 // launch of the multi-workgroup kernel, PITON_GEMM_DIRECT_WAVES workgroups per CU)
@@ -538,18 +559,22 @@ void gemm_direct_kernel(GemmArgs g) {
 constexpr int kMaxSplitWaves = PITON_SPLIT_MAX_WAVES;
 enum SplitA { A_ROW16 = 0, A_ROW = 1, A_COL = 2 };
 
-template <int NB, int KS, int AM, bool BKC>
+template <int NB, int NBN, int KS, int AM, bool BKC>
 __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     constexpr bool AVEC = AM == A_ROW16;
-    constexpr int TB = 32 * NB;
-    constexpr int NACC = NB * NB * 16;  // accumulator registers per lane
-    __shared__ float red[KS > 1 ? KS : 1][NACC][64];
+    constexpr int TB = 32 * NB, TBN = 32 * NBN;  // tile rows and columns
+    constexpr int NACC = NB * NBN * 16;          // accumulator registers per lane
+    // the partial tiles: [wave][group of four accumulators][lane], 16 bytes per lane and group
+    __shared__ f32x4 red[KS > 1 ? KS : 1][NACC / 4][64];
+    keep_epilogue_args(g);
     // the wave index is uniform: readfirstlane makes the K loop, which starts at it, a scalar loop
     const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
     const int half = lane >> 5, l31 = lane & 31;
+    PITON_PHASE_VARS;
+    PITON_PHASE(0);
 
     const int num_pid_m = (int)((g.M + TB - 1) / TB);
-    const int num_pid_n = (int)((g.N + TB - 1) / TB);
+    const int num_pid_n = (int)((g.N + TBN - 1) / TBN);
     const int pid = xcd_logical_id(blockIdx.x, gridDim.x, kXcdCount);
     const int in_group = g.group_m * num_pid_n;
     const int group_id = pid / in_group;
@@ -557,7 +582,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     const int gsize = min(num_pid_m - first_m, g.group_m);
     const int pid_m = first_m + (pid % in_group) % gsize;
     const int pid_n = (pid % in_group) / gsize;
-    const int64_t m0 = (int64_t)pid_m * TB, n0 = (int64_t)pid_n * TB;
+    const int64_t m0 = (int64_t)pid_m * TB, n0 = (int64_t)pid_n * TBN;
 
     // the stride along each operand's contiguous axis is 1 (the host checks it)
     const int64_t s_am = AM == A_COL ? 1 : g.s_am, s_ak = AM == A_COL ? g.s_ak : 1;
@@ -574,7 +599,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
                                                       (int)(((a_end + 3) & ~(int64_t)3) * 4), 0x00020000);
     const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.b), (short)0,
                                                       (int)(((g.K - 1) * s_bk + (g.N - 1) * s_bn + 1) * 4), 0x00020000);
-    uint32_t va[NB], vb[NB];
+    uint32_t va[NB], vb[NBN];
     int ra_shift[NB];  // A_ROW: this lane's row start past its 16-byte boundary, in floats
 #pragma unroll
     for (int i = 0; i < NB; i++) {
@@ -583,31 +608,37 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
         va[i] = (uint32_t)((AM == A_COL ? e0 : e0 & ~(int64_t)3) * 4);
     }
 #pragma unroll
-    for (int j = 0; j < NB; j++) vb[j] = (uint32_t)(((int64_t)(16 * half) * s_bk + (n0 + j * 32 + l31) * s_bn) * 4);
+    for (int j = 0; j < NBN; j++) vb[j] = (uint32_t)(((int64_t)(16 * half) * s_bk + (n0 + j * 32 + l31) * s_bn) * 4);
     const uint32_t sak4 = (uint32_t)(s_ak * 4), sbk4 = (uint32_t)(s_bk * 4);
     const int nk = (int)((g.K + 31) / 32);
 
     constexpr int AW = AM == A_ROW ? 20 : 16;  // A floats a lane loads per block and tile
     struct Ops {
         float a[NB][AW];
-        float b[NB][16];
+        float b[NBN][16];
     };
     // every offset goes in the per-lane address, which is what the descriptor's range check
     // covers. The K tail: a row-major A's elements and a column-major B's with k >= K get an
     // offset past the bound (2^31, beyond any bound of a matrix under 2 GiB), so they read as zero
     // with no data dependence; a column-major A's and a row-major B's lie past the bound already.
     constexpr uint32_t kOut = 0x80000000u;
-    auto load = [&](int kt, Ops &o) {
+    // PIN keeps the loads in source order with scheduling barriers (A first, then B step by step).
+    auto load = [&](int kt, Ops &o, auto pin) {
         const uint32_t ka = (uint32_t)kt * 32u * sak4, kb = (uint32_t)kt * 32u * sbk4;
         const int64_t k0 = (int64_t)kt * 32 + 16 * half;  // this lane's first k of the tile
+        auto pinned = [&]() {
+            if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
+        };
 #pragma unroll
         for (int i = 0; i < NB; i++) {
             if constexpr (AM == A_COL) {
                 // columns no closer than M floats apart (the host checks it): (m, k) with k >= K
                 // lies at or past (K - 1) s_ak + M, the bound
 #pragma unroll
-                for (int s = 0; s < 16; s++)
+                for (int s = 0; s < 16; s++) {
                     o.a[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)(va[i] + ka + s * sak4), 0, 0));
+                    pinned();
+                }
             } else if constexpr (AVEC) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -615,6 +646,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
                     const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0));
 #pragma unroll
                     for (int e = 0; e < 4; e++) o.a[i][4 * q + e] = v[e];
+                    pinned();
                 }
             } else {
                 // the chunks holding k0 - r .. k0 - r + 19; the K tail is zeroed in mul
@@ -624,32 +656,38 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
                     const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0));
 #pragma unroll
                     for (int e = 0; e < 4; e++) o.a[i][4 * q + e] = v[e];
+                    pinned();
                 }
             }
         }
         if constexpr (BKC) {
 #pragma unroll
-            for (int j = 0; j < NB; j++)
+            for (int j = 0; j < NBN; j++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const uint32_t off = k0 + 4 * q < g.K ? vb[j] + kb + 16 * q : kOut;
                     const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0));
 #pragma unroll
                     for (int e = 0; e < 4; e++) o.b[j][4 * q + e] = v[e];
+                    pinned();
                 }
         } else {
 #pragma unroll
             for (int s = 0; s < 16; s++)
 #pragma unroll
-                for (int j = 0; j < NB; j++)
+                for (int j = 0; j < NBN; j++) {
                     o.b[j][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)(vb[j] + kb + s * sbk4), 0, 0));
+                    pinned();
+                }
         }
     };
-    f32x16 acc[NB][NB];
+    using Pin = std::true_type;
+    using Free = std::false_type;
+    f32x16 acc[NB][NBN];
 #pragma unroll
     for (int i = 0; i < NB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++)
+        for (int j = 0; j < NBN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
     // A_ROW: the lane's 16 values of block i: window[s + r], zero where k0 + s >= K
@@ -685,7 +723,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < NB; i++)
 #pragma unroll
-                for (int j = 0; j < NB; j++)
+                for (int j = 0; j < NBN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], o.b[j][s], acc[i][j], 0, 0, 0);
     };
     // this wave's K tiles: wave, wave + KS, ...; the next one is in flight while one multiplies.
@@ -703,8 +741,11 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
 #ifndef PITON_SPLIT_LPM
 #define PITON_SPLIT_LPM 1
 #endif
-    constexpr int LOADS = NB * (AM == A_ROW16 ? 4 : AM == A_ROW ? 5 : 16) + NB * (BKC ? 4 : 16);
-    constexpr int MFMAS = 16 * NB * NB, LPM = PITON_SPLIT_LPM;
+    // 32 x 32 tiles (NB = 1): 20 loads against 16 MFMAs, two after each so that every load is in
+    // flight before the tile's last product (512^3: 6.04 -> 5.72 us; 64 x 64 tiles keep one:
+    // 1024^3 20.9 against 21.7 us with two, 22.4 with three)
+    constexpr int LOADS = NB * (AM == A_ROW16 ? 4 : AM == A_ROW ? 5 : 16) + NBN * (BKC ? 4 : 16);
+    constexpr int MFMAS = 16 * NB * NBN, LPM = NB == 1 ? 2 : PITON_SPLIT_LPM;
     auto interleave = [&]() {
 #pragma unroll
         for (int i = 0; i < MFMAS; i++) {
@@ -712,19 +753,35 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
             if (i * LPM < LOADS) __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);  // LPM VMEM reads
         }
     };
+    // Each half starts with every load of its tile landed (vmcnt(0)): its tile's loads went out
+    // during the other half, and waiting only for the first of them would let the next tile's
+    // loads join them, 80 in flight against the 63 a wave's vector-memory counter tracks, which
+    // stalls the issue of loads and products alike (1024^2 x 4096: 69.0 -> 77.7 us).
+    // The prologue's loads go out in source order on 32 x 32 tiles (a wave has few K tiles, and
+    // the first products start when their operands arrive: 512^3 5.72 -> 5.6 us); on 64 x 64
+    // tiles that order measured slower in the loop that follows (1024^2 x 4096: 77 against 69 us,
+    // the same instructions in another register assignment), so the compiler orders them.
     Ops o0, o1;
-    load(wave, o0);
+    if constexpr (NB == 1) load(wave, o0, Pin());
+    else load(wave, o0, Free());
+    PITON_PHASE_WAIT_LOADS();
+    PITON_PHASE(1);
     for (int kt = wave; kt < nk; kt += 2 * KS) {
-        load(kt + KS, o1);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __builtin_amdgcn_sched_barrier(0);
+        load(kt + KS, o1, Free());
         mul(o0, kt);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
-        load(kt + 2 * KS, o0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __builtin_amdgcn_sched_barrier(0);
+        load(kt + 2 * KS, o0, Free());
         mul(o1, kt + KS);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
     }
 
+    PITON_PHASE(2);
     // accumulator r of a 32x32 block holds row 8*(r/4) + 4*half + r%4, column l31
     auto store = [&](int i, int j, int r, int ln, float v) {
         const int64_t row = m0 + i * 32 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
@@ -739,25 +796,45 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < NB; i++)
 #pragma unroll
-            for (int j = 0; j < NB; j++)
+            for (int j = 0; j < NBN; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) store(i, j, r, lane, acc[i][j][r]);
     } else {
 #pragma unroll
         for (int i = 0; i < NB; i++)
 #pragma unroll
-            for (int j = 0; j < NB; j++)
+            for (int j = 0; j < NBN; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) red[wave][(i * NB + j) * 16 + r][lane] = acc[i][j][r];
-        __syncthreads();
-        // wave w finishes accumulator slots w, w + KS, ...: the partials add in wave order
-        for (int x = wave; x < NACC; x += KS) {
-            float v = red[0][x][lane];
+                for (int q = 0; q < 4; q++)
+                    red[wave][(i * NBN + j) * 4 + q][lane] =
+                        f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        // an LDS-only barrier: the partials are in LDS; nothing here waits for other memory
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kWaitcntLgkm0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        __builtin_amdgcn_sched_barrier(0);
+        // wave w finishes the groups w, w + KS, ... of four accumulators, every partial read
+        // first; the partials add in wave order
+        constexpr int GPW = NACC / 4 / KS;  // groups per wave
+        f32x4 part[GPW][KS];
 #pragma unroll
-            for (int w = 1; w < KS; w++) v += red[w][x][lane];
-            store((x >> 4) / NB, (x >> 4) % NB, x & 15, lane, v);
+        for (int u = 0; u < GPW; u++)
+#pragma unroll
+            for (int w = 0; w < KS; w++) part[u][w] = red[w][wave + KS * u][lane];
+#pragma unroll
+        for (int u = 0; u < GPW; u++) {
+            const int x = wave + KS * u;  // group: block x / 4, accumulators 4 (x % 4) .. + 3
+            f32x4 v = part[u][0];
+#pragma unroll
+            for (int w = 1; w < KS; w++) v += part[u][w];
+#pragma unroll
+            for (int e = 0; e < 4; e++) store((x >> 2) / NBN, (x >> 2) % NBN, 4 * (x & 3) + e, lane, v[e]);
         }
     }
+    PITON_PHASE(3);
+    PITON_PHASE_END(kPhaseGemmSplit, g.phase);
 }
 
 // First index of the largest of x[r, 0:n] (numpy argmax rule: the first NaN wins), one wave
@@ -802,6 +879,7 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 // would have written. Needs the FAST layout.
 template <bool FAST, bool LN>
 __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) {
+    keep_epilogue_args(g);
     static_assert(!LN || FAST, "LN needs the FAST layout");
     __shared__ float part[SMWAVES][4][64];  // [wave][accumulator][lane]: 16 KiB
     __shared__ float stats[16][2];          // LN: mean and 1/sqrt(var + eps) of the tile's rows
@@ -963,9 +1041,10 @@ struct SplitPlan {
     int64_t tiles;
     int am;    // SplitA: A's layout
     bool bkc;  // B column-major
+    int nbn;   // blocks of 32 columns per tile (nb, or 2 nb: the wide tile)
 };
 static SplitPlan plan_split(const GemmArgs &g, int cus) {
-    SplitPlan p{0, 0, 0, A_ROW16, false};
+    SplitPlan p{0, 0, 0, A_ROW16, false, 0};
     if (g.K <= 0 || g.M <= 0 || g.N <= 0) return p;
     // A with stride 1 along K (16-byte loads where its rows are 16-byte aligned and K % 4 == 0) or
     // along M with columns at least M floats apart; B with stride 1 along N, or along K with
@@ -976,7 +1055,8 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     if (g.s_bn == 1 && g.s_bk > 0) p.bkc = false;
     else if (g.s_bk == 1 && g.s_bn > 0 && g.s_bn % 4 == 0 && g.K % 4 == 0 && aligned16(g.b)) p.bkc = true;
     else return p;
-    auto tiles = [&](int64_t tb) { return sat_mul((g.M + tb - 1) / tb, (g.N + tb - 1) / tb); };
+    auto tiles2 = [&](int64_t tm, int64_t tn) { return sat_mul((g.M + tm - 1) / tm, (g.N + tn - 1) / tn); };
+    auto tiles = [&](int64_t tb) { return tiles2(tb, tb); };
     const int64_t nk = (g.K + 31) / 32;
 #ifndef PITON_SPLIT_NB_MAX
 #define PITON_SPLIT_NB_MAX 2
@@ -990,29 +1070,58 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     if (sat_add(sat_mul(g.M + tb, g.s_am), sat_mul(kpad, g.s_ak)) >= (1LL << 29) - 4 ||
         sat_add(sat_mul(kpad, g.s_bk), sat_mul(g.N + tb, g.s_bn)) >= (1LL << 29) || nt > 0x7FFFFFFF)
         return p;
-    p.nb = nb, p.ks = ks, p.tiles = nt;
+    p.nb = nb, p.ks = ks, p.tiles = nt, p.nbn = nb;
+    // the wide tile, 64 x 128: where 64 x 64 tiles would put two workgroups on some CUs and the
+    // 64 x 128 ones fit one per CU (the ragged 1000 x 1800 x 700: 464 against 240), four waves
+    // splitting K give each SIMD one wave with the same MFMA work as two waves of the square
+    // tile, and the wave's 2 x 4 blocks need 0.56 loads per product instead of 0.63
+    const int64_t ntw = tiles2(64, 128);
+    // (measured where A's rows are 16-byte aligned and B is row-major: 2048 x 768 x 256 15.9 ->
+    // 15.4 us, 1024 x 2048 x 256 16.3 -> 15.8; the same on the aligned ragged shape; 2-3 % slower
+    // with A's rows unaligned or B column-major, which keep the square tile)
+    if (nb == 2 && ks == 4 && nt > cus && ntw <= cus && p.am == A_ROW16 && !p.bkc && PITON_SPLIT_WIDE &&
+        sat_add(sat_mul(kpad, g.s_bk), sat_mul(g.N + 128, g.s_bn)) < (1LL << 29)) {
+        p.nbn = 4;
+        p.tiles = ntw;
+    }
     return p;
 }
 
-template <int NB, int KS>
+// the recorded name of gemm_split_kernel<NB, NBN, KS, AM, BKC>, with its parameters' values
+template <int NB, int NBN, int KS, int AM, bool BKC>
+static const char *split_name() {
+    static const std::string name = "gemm_split_kernel<" + std::to_string(NB) + ", " + std::to_string(NBN) + ", " +
+                                    std::to_string(KS) + ", " +
+                                    (AM == A_ROW16 ? "A_ROW16" : AM == A_ROW ? "A_ROW" : "A_COL") + ", " +
+                                    (BKC ? "true" : "false") + ">";
+    return name.c_str();
+}
+
+template <int NB, int NBN, int KS, int AM, bool BKC>
+static void launch_split_one(const GemmArgs &g, unsigned nwg, hipStream_t st) {
+    PITON_LAUNCH_NAMED((gemm_split_kernel<NB, NBN, KS, AM, BKC>), (split_name<NB, NBN, KS, AM, BKC>()), dim3(nwg),
+                       dim3(64 * KS), 0, st, g);
+}
+
+template <int NB, int NBN, int KS>
 static void launch_split_ks(const GemmArgs &g, int am, bool bkc, unsigned nwg, hipStream_t st) {
-    const dim3 grid(nwg), block(64 * KS);
-    if (am == A_ROW16 && !bkc) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_ROW16, false>), grid, block, 0, st, g);
-    else if (am == A_ROW16) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_ROW16, true>), grid, block, 0, st, g);
-    else if (am == A_ROW && !bkc) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_ROW, false>), grid, block, 0, st, g);
-    else if (am == A_ROW) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_ROW, true>), grid, block, 0, st, g);
-    else if (!bkc) PITON_LAUNCH((gemm_split_kernel<NB, KS, A_COL, false>), grid, block, 0, st, g);
-    else PITON_LAUNCH((gemm_split_kernel<NB, KS, A_COL, true>), grid, block, 0, st, g);
+    if (am == A_ROW16 && !bkc) launch_split_one<NB, NBN, KS, A_ROW16, false>(g, nwg, st);
+    else if (am == A_ROW16) launch_split_one<NB, NBN, KS, A_ROW16, true>(g, nwg, st);
+    else if (am == A_ROW && !bkc) launch_split_one<NB, NBN, KS, A_ROW, false>(g, nwg, st);
+    else if (am == A_ROW) launch_split_one<NB, NBN, KS, A_ROW, true>(g, nwg, st);
+    else if (!bkc) launch_split_one<NB, NBN, KS, A_COL, false>(g, nwg, st);
+    else launch_split_one<NB, NBN, KS, A_COL, true>(g, nwg, st);
 }
 
 template <int NB>
 static void launch_split_nb(const GemmArgs &g, const SplitPlan &sp, unsigned nwg, hipStream_t st) {
-    if (sp.ks == 1) launch_split_ks<NB, 1>(g, sp.am, sp.bkc, nwg, st);
-    else if (sp.ks == 2) launch_split_ks<NB, 2>(g, sp.am, sp.bkc, nwg, st);
+    if (sp.ks == 1) launch_split_ks<NB, NB, 1>(g, sp.am, sp.bkc, nwg, st);
+    else if (sp.ks == 2) launch_split_ks<NB, NB, 2>(g, sp.am, sp.bkc, nwg, st);
 #if PITON_SPLIT_MAX_WAVES > 4
-    else if (sp.ks == 8) launch_split_ks<NB, 8>(g, sp.am, sp.bkc, nwg, st);
+    else if (sp.ks == 8) launch_split_ks<NB, NB, 8>(g, sp.am, sp.bkc, nwg, st);
 #endif
-    else launch_split_ks<NB, 4>(g, sp.am, sp.bkc, nwg, st);
+    else if (NB == 2 && sp.nbn == 4) launch_split_ks<2, 4, 4>(g, sp.am, sp.bkc, nwg, st);
+    else launch_split_ks<NB, NB, 4>(g, sp.am, sp.bkc, nwg, st);
 }
 
 template <int A_L>
@@ -1088,6 +1197,7 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
         const int64_t rows = (g.M + 32 * sp.nb - 1) / (32 * sp.nb);
         GemmArgs gs = g;
         gs.group_m = (int)(group_user > rows ? rows : group_user);
+        gs.phase = phase_slot();
         if (sp.nb == 2) launch_split_nb<2>(gs, sp, (unsigned)sp.tiles, st);
         else launch_split_nb<1>(gs, sp, (unsigned)sp.tiles, st);
     } else if (direct) {
@@ -1113,6 +1223,8 @@ static int launch_gemm(GemmArgs g, hipStream_t st, const char *what, bool split_
 }
 
 }  // namespace piton
+
+PITON_PHASE_TU(matmul)
 
 extern "C" {
 

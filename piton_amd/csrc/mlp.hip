@@ -133,6 +133,10 @@ __global__ __launch_bounds__(256) void mlp3_rows16_kernel(const float *x, int64_
     const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
     const int grp = lane >> 4, c16 = lane & 15;
     const int64_t r0 = (int64_t)blockIdx.x * 16;
+    // the epilogue's arguments, read with the others at the start
+    logits = sgpr_keep(logits);
+    pred = sgpr_keep(pred);
+    n_classes = sgpr_keep(n_classes);
     PITON_PHASE_VARS;
     PITON_PHASE(0);
     // the row this lane supplies to layer 1's A operand: a row past M reads row M - 1 instead
@@ -247,11 +251,16 @@ __global__ __launch_bounds__(256) void mlp3_rows16_kernel(const float *x, int64_
         float lv[N3];
 #pragma unroll
         for (int c = 0; c < N3; c++) lv[c] = lg[lane][c];
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
+        // in class order, numpy's rule is: the first NaN wins, else a strictly larger value
+        // (selects only: the general combine's branches cost more than the ten comparisons)
+        float bv = lv[0];
+        int bi = 0;
 #pragma unroll
-        for (int c = 0; c < N3; c++)
-            if (c < n_classes) argmax_combine(bv, bi, lv[c], c);
+        for (int c = 1; c < N3; c++) {
+            const bool take = c < n_classes && bv == bv && (lv[c] != lv[c] || lv[c] > bv);
+            bv = take ? lv[c] : bv;
+            bi = take ? c : bi;
+        }
         pred[r0 + lane] = bi;
     }
     PITON_PHASE(3);

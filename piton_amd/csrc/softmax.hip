@@ -59,11 +59,13 @@ __device__ __forceinline__ float exp_row(float d) {
     return __builtin_amdgcn_exp2f(d * kL2E);
 }
 
-// The emulator's view of an operand for the row maximum and the subtraction: a NaN with the
-// sign bit set (bits above 0xFF800000) is -inf; every other value is itself (a +NaN stays NaN,
-// so the row still comes out NaN). Two VALU operations per element of an HBM-bound kernel.
+// The emulator's view of an operand of the subtraction x - max: a NaN with the sign bit set
+// (bits above 0xFF800000 as an unsigned integer) is -inf, every other value is itself (a +NaN
+// stays NaN, so its row still comes out NaN): one v_min_u32. The row maximum needs no mapping:
+// IEEE max returns the other operand of a NaN, as max over the mapped values would (a row of
+// -NaN and -inf only has maximum -inf either way).
 __device__ __forceinline__ float qpu_neg_nan(float x) {
-    return __float_as_uint(x) > 0xFF800000u ? -INFINITY : x;
+    return __uint_as_float(min(__float_as_uint(x), 0xFF800000u));
 }
 
 // Loads row r's aligned float4 window into b: T threads share the row, thread t holding
@@ -122,8 +124,6 @@ __device__ __forceinline__ void softmax_store_row(float *out, int64_t out_rs, in
             for (int j = 0; j < 4; j++)
                 if (!(e0 + j >= 0 && e0 + j < n)) b[c][j] = -INFINITY;
         }
-#pragma unroll
-        for (int j = 0; j < 4; j++) b[c][j] = qpu_neg_nan(b[c][j]);
         mx = fmaxf(mx, fmaxf(fmaxf(b[c].x, b[c].y), fmaxf(b[c].z, b[c].w)));
     }
     const float m = row_reduce<T>(mx, MaxOp(), red);
@@ -133,8 +133,9 @@ __device__ __forceinline__ void softmax_store_row(float *out, int64_t out_rs, in
     for (int c = 0; c < CH; c++) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            // masked entries hold -inf: exactly 0 here unless the row itself is NaN
-            const float e = exp_row(b[c][j] - m);
+            // masked entries hold -inf, and so do -NaN entries (qpu_neg_nan): exactly 0 here
+            // unless the row itself is NaN
+            const float e = exp_row(qpu_neg_nan(b[c][j]) - m);
             b[c][j] = e;
             s += e;
         }
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(float *out, const flo
     const float *rp = in + row * in_rs;
     float *op = out + row * out_rs;
     float mx = -INFINITY;
-    for (int64_t i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, qpu_neg_nan(rp[i]));
+    for (int64_t i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, rp[i]);
     const float m = block_reduce(mx, red, true);
     float s = 0.f;
     for (int64_t i = threadIdx.x; i < n; i += 256) s += exp_row(qpu_neg_nan(rp[i]) - m);

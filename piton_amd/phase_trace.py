@@ -1,5 +1,6 @@
 """Launch phases of the HBM-bound softmax, the one-generation attention kernel, the decode
-attention of the KV-cached decoder, its fused decode step and the digits MLP (diagnostics).
+attention of the KV-cached decoder, its fused decode step, the split GEMM of the small and
+ragged matmul shapes and the digits MLP (diagnostics).
 
 `python -m piton_amd.phase_trace` builds a traced copy of the library beside the product one
 (-DPITON_PHASE_TRACE: every traced wave keeps s_memrealtime stamps -- a 100 MHz clock shared by
@@ -197,6 +198,32 @@ def mlp_phases(batch: int, launches: int = 12):
     return {key: statistics.median(r[key] for r in rows) * (1 if key == "waves" else TICK_US) for key in rows[0]}
 
 
+def gemm_split_phases(M: int, N: int, K: int, lda: int, ldb: int, ldc: int, launches: int = 12):
+    """The split GEMM (the small and ragged matmul shapes) on U[-1, 1] inputs: per launch, the
+    last wave's start, medians over waves of the wait for the first K tile's operands, of the K
+    loop and of the partial-tile sum and stores, and when the last wave ends."""
+    import torch
+
+    from .runtime import mi355x as rt
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    a = torch.rand((M, lda), device="cuda", generator=g) * 2 - 1
+    b = torch.rand((K, ldb), device="cuda", generator=g) * 2 - 1
+    c = torch.empty((M, ldc), device="cuda")
+    per = _trace("matmul", lambda i: rt.matmul(a, b, c, M, N, K, lda, 1, ldb, 1, ldc, 1, 8), launches)
+    rows = []
+    for k in range(1, len(per) - 1):
+        ls = per[k]
+        t0 = min(r[0] for r in ls)
+        rows.append(dict(waves=len(ls), last_wave_start=max(r[0] for r in ls) - t0,
+                         first_tile=statistics.median(r[1] - r[0] for r in ls),
+                         loop=statistics.median(r[2] - r[1] for r in ls),
+                         loop_max=max(r[2] - r[1] for r in ls),
+                         epilogue=statistics.median(r[3] - r[2] for r in ls),
+                         end=max(r[3] for r in ls) - t0,
+                         gap_to_next=min(r[0] for r in per[k + 1]) - max(r[3] for r in ls)))
+    return {key: statistics.median(r[key] for r in rows) * (1 if key == "waves" else TICK_US) for key in rows[0]}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--no-build", action="store_true", help="use the traced library already built")
@@ -232,6 +259,16 @@ def main():
         m = decode_layer_phases(nk)
         print(f"| {nk} keys | {us(m['layernorm'])} | {us(m['projection'])} | {us(m['cache_copies'])} | "
               f"{us(m['attention'])} | {us(m['end'])} | {us(m['gap_to_next'])} |")
+    print()
+    print("| split GEMM | waves | last wave starts | first K tile in | K loop (median / max) | partial-tile sum "
+          "and stores | last wave ends | gap to next launch |")
+    print("|---|---|---|---|---|---|---|---|")
+    for shape in ((512, 512, 512, 512, 512, 512), (1024, 1024, 1024, 1024, 1024, 1024),
+                  (1000, 1800, 700, 703, 1805, 1807)):
+        m = gemm_split_phases(*shape)
+        print(f"| {shape[0]} x {shape[1]} x {shape[2]} | {int(m['waves'])} | {us(m['last_wave_start'])} | "
+              f"{us(m['first_tile'])} | {us(m['loop'])} / {us(m['loop_max'])} | {us(m['epilogue'])} | "
+              f"{us(m['end'])} | {us(m['gap_to_next'])} |")
     print()
     print("| digits MLP, one launch | waves | last wave starts | every operand in | layers 1 and 2 | "
           "layer 3 and argmax (wave 0) | last wave ends | gap to next launch |")

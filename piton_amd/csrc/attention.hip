@@ -752,6 +752,16 @@ struct DecodeArgs {
     PhaseRecord *phase;  // the launch's phase-trace records (diagnostics builds; null otherwise)
 };
 
+// Holds the arguments read after the scores (the scale, the output and its strides) in scalar
+// registers from the start: the compiler would otherwise load them from the kernarg segment
+// where they are first used, one more memory round trip on the critical path.
+__device__ __forceinline__ void keep_decode_args(DecodeArgs &g) {
+    g.scale = sgpr_keep(g.scale);
+    g.o = sgpr_keep(g.o);
+    g.s_ob = sgpr_keep(g.s_ob);
+    g.s_oh = sgpr_keep(g.s_oh);
+}
+
 template <class Op>
 __device__ __forceinline__ float block_reduce4(float v, Op op, float *red) {
     v = wave_reduce(v, op);
@@ -762,6 +772,7 @@ __device__ __forceinline__ float block_reduce4(float v, Op op, float *red) {
 
 template <int D, bool VEC>
 __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeArgs g) {
+    keep_decode_args(g);
     __shared__ float p[kMaxDecodeKeys];
     __shared__ float red[8];
     __shared__ float part[256];
@@ -840,6 +851,7 @@ constexpr int kShortDecodeKeys = 256;
 
 template <int D, bool VEC>
 __global__ __launch_bounds__(256) void attn_decode_short(DecodeArgs g) {
+    keep_decode_args(g);
     static_assert(D <= 64, "short decode holds K and V in registers for head_dim <= 64");
     __shared__ float p[kShortDecodeKeys];
     __shared__ float red[8];

@@ -390,6 +390,11 @@ struct LmHeadArgs {
 };
 
 __global__ __launch_bounds__(kDlThreads) void lm_head_kernel(LmHeadArgs g) {
+    // read with the other arguments, not reloaded where they are first used
+    g.eps = sgpr_keep(g.eps);
+    g.logits = sgpr_keep(g.logits);
+    g.next = sgpr_keep(g.next);
+    g.n_classes = sgpr_keep(g.n_classes);
     constexpr int kMaxN = kDlMaxModel, NJ = kMaxN / kDlThreads;
     __shared__ __attribute__((aligned(16))) float lnx[kDlMaxModel];
     __shared__ __attribute__((aligned(16))) float gp[kDlWaves][kMaxN];

@@ -25,6 +25,8 @@ __global__ __launch_bounds__(256) void add_scalar_kernel(const float *x, const f
 template <int CH>
 __global__ __launch_bounds__(256) void layernorm_rows_kernel(const float *x, float *out, int64_t n, float eps,
                                                              int64_t rows, int64_t rs) {
+    eps = sgpr_keep(eps);  // read with the other arguments, not reloaded after the mean
+    out = sgpr_keep(out);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + wave;
     if (row >= rows) return;

@@ -50,7 +50,8 @@ struct GemmArgs {
     PhaseRecord *phase;    // split kernel: the launch's phase-trace records (diagnostics builds; null otherwise)
 };
 
-// Holds the epilogue's arguments (C and its strides, bias, ReLU, residual) in scalar registers
+// Holds the epilogue's arguments (C and its strides, bias, ReLU, residual; the layernorm's eps)
+// in scalar registers
 // from the kernel's start: otherwise the compiler reloads them from the kernarg segment at the
 // epilogue, one more memory round trip at the end of every launch.
 __device__ __forceinline__ void keep_epilogue_args(GemmArgs &g) {
@@ -61,6 +62,7 @@ __device__ __forceinline__ void keep_epilogue_args(GemmArgs &g) {
     g.relu = sgpr_keep(g.relu);
     g.res = sgpr_keep(g.res);
     g.s_rm = sgpr_keep(g.s_rm);
+    g.ln_eps = sgpr_keep(g.ln_eps);
 }
 
 // Loads the A tile (GBM x GBK at m0, k0) into 16 registers per thread.
@@ -842,6 +844,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
 // across the wave with argmax_combine (common.h), whose result does not depend on the order.
 
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const float *x, int64_t rows, int64_t ld, int n, int32_t *out) {
+    out = sgpr_keep(out);  // read with the other arguments, not reloaded at the store
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (r >= rows) return;  // whole wavefront leaves together

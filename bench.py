@@ -53,6 +53,11 @@ def parse():
 
 
 CAL_ELEMS = 64 * 2 ** 20  # calibration add: reads 2 x 256 MiB, writes 256 MiB
+# the matmul config's other shapes: (M, N, K, lda, ldb, ldc, B column-major); the ragged one with
+# rows of A, B and C not 16-byte aligned
+MATMUL_SHAPES = [(512, 512, 512, 512, 512, 512, False), (1024, 1024, 1024, 1024, 1024, 1024, False),
+                 (1000, 1800, 700, 703, 1805, 1807, False), (1024, 1024, 1024, 1024, 1024, 1024, True),
+                 (4096, 4096, 4096, 4096, 4096, 4096, True)]
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_bench_kernels.json")
 
 
@@ -152,6 +157,23 @@ def pmc_probe(n):
     for _ in range(2):
         rt.attn_fwd(q, k, v, o, 0.125, 65536, 64, 65536, 64, 1, 65536, 64, 65536, 64, 1024, 32, 64, True)
     torch.cuda.synchronize()
+    del q, k, v, o
+    # the matmul config's other shapes (the split GEMM), as bench_matmul_shape lays them out
+    for (M, N, K, lda, ldb, ldc, bt) in MATMUL_SHAPES[:4]:
+        A = torch.rand((M, lda), device="cuda") * 2 - 1
+        B = torch.rand((N, ldb) if bt else (K, ldb), device="cuda") * 2 - 1
+        C = torch.empty((M, ldc), device="cuda")
+        s_bk, s_bn = (1, ldb) if bt else (ldb, 1)
+        for _ in range(2):
+            rt.matmul(A, B, C, M, N, K, lda, 1, s_bk, s_bn, ldc, 1, 8)
+        torch.cuda.synchronize()
+    # the digits MLP over 1797 images
+    from piton_amd import digits
+    mlp = digits.MLP(digits.he_normal_mlp(seed=1729), max_batch=1797)
+    x = torch.randint(0, 17, (1797, 64), device="cuda").float()
+    for _ in range(2):
+        mlp.run(x)
+    torch.cuda.synchronize()
 
 
 def timed_graph(fn, iters, reps=5):
@@ -224,9 +246,16 @@ def bench_matmul_shape(M, N, K, lda, ldb, ldc, launches=32, b_transposed=False):
     kernel = " + ".join(f"{l['kernel']} x {l['grid'][0]}" for l in rt.last_launches())
     avg = timed_graph(step, launches)
     flops = 2.0 * M * N * K
-    return dict(M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, b_transposed=b_transposed, kernel=kernel,
+    line = dict(M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, b_transposed=b_transposed, kernel=kernel,
                 us=round(avg * 1e6, 3), tflops=round(flops / avg / 1e12, 3),
                 frac_mfma=round(flops / avg / PEAK_FP32_MFMA, 4))
+    # HBM bytes per launch from the committed counter passes, where they cover the shape
+    label = {(512, 512, 512, 512, False): "matmul 512^3", (1024, 1024, 1024, 1024, False): "matmul 1024^3",
+             (1000, 1800, 700, 703, False): "matmul 1000 x 1800 x 700 (row strides 703 / 1805 / 1807)",
+             (1024, 1024, 1024, 1024, True): "matmul 1024^3, B column-major"}.get((M, N, K, lda, b_transposed))
+    if label:
+        line["traffic"] = measured_traffic(label)
+    return line
 
 
 def bench_softmax(n, rows=4096, launches=48, sample_rows=256):
@@ -649,10 +678,8 @@ def main():
     torch.cuda.empty_cache()
     samples = {}
     if not args.no_extras:
-        line["matmul_shapes"] = [bench_matmul_shape(s, s, s, s, s, s) for s in (512, 1024)] + \
-            [bench_matmul_shape(1000, 1800, 700, 703, 1805, 1807)] + \
-            [bench_matmul_shape(s, s, s, s, s, s, launches=8 if s == 4096 else 32, b_transposed=True)
-             for s in (1024, 4096)]
+        line["matmul_shapes"] = [bench_matmul_shape(*sh[:6], launches=8 if sh[0] == 4096 else 32, b_transposed=sh[6])
+                                 for sh in MATMUL_SHAPES]
         line["softmax"] = []
         for nc in (1024, 4096, 1823):
             sm, samples[f"softmax {nc}"] = bench_softmax(nc)

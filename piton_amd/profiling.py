@@ -1,7 +1,7 @@
 """Summaries of rocprofv3 output for the benchmark kernels.
 
     python -m piton_amd.profiling KT_DIR FETCH_DIR WRITE_DIR [--json OUT]
-    python -m piton_amd.profiling PMC_DIR --mfma
+    python -m piton_amd.profiling PMC_DIR --mfma [--trace KT_DIR --clock GHZ]
 
 KT_DIR holds a `--kernel-trace --stats` run of `python3 bench.py` (*_kernel_trace.csv);
 FETCH_DIR / WRITE_DIR hold `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of
@@ -11,7 +11,8 @@ launches), and its HBM traffic per step, each counter scaled by the factor that 
 calibration add of known size (bench.py CAL_ELEMS: reads 2 x 256 MiB, writes 256 MiB) onto its
 true bytes. --json writes {workload: {fetch_bytes, write_bytes, ...}}.
 With --mfma, PMC_DIR holds a `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES` run of
-`python3 bench.py --pmc-probe`: the MFMA pipe occupancy of the benchmark's MFMA workloads.
+`python3 bench.py --pmc-probe`: the MFMA pipe occupancy of the benchmark's MFMA workloads, per
+cycle of each dispatch's own span and per cycle of the counter window.
 With --lds, PMC_DIR holds a `--pmc GRBM_GUI_ACTIVE SQ_WAVE_CYCLES SQ_LDS_IDX_ACTIVE
 SQ_LDS_BANK_CONFLICT` run of the same: each workload's mean resident waves per SIMD and its LDS
 bank-conflict cycles per conflict-free LDS cycle.
@@ -29,23 +30,44 @@ import sys
 CAL_READ = 2 * 64 * 2 ** 20 * 4
 CAL_WRITE = 64 * 2 ** 20 * 4
 
+def _mm(M, N, K):
+    return (4 * (M * K + K * N + M * N), 2 * M * N * K)
+
+
+# the digits MLP over 1797 images: x, the three layers' weights and biases, logits and predictions
+_MLP_BYTES = 4 * (1797 * 64 + 64 * 128 + 128 + 128 * 64 + 64 + 64 * 10 + 10 + 1797 * 10 + 1797)
+_MLP_FLOPS = 2 * 1797 * (64 * 128 + 128 * 64 + 64 * 10)
+
 # benchmark workloads: (algorithmic HBM bytes per step, algorithmic FLOPs per step)
 WORKLOADS = {
-    "matmul 4096^3": (3 * 4096 * 4096 * 4, 2 * 4096 ** 3),
+    "matmul 4096^3": _mm(4096, 4096, 4096),
+    "matmul 512^3": _mm(512, 512, 512),
+    "matmul 1024^3": _mm(1024, 1024, 1024),
+    "matmul 1000 x 1800 x 700 (row strides 703 / 1805 / 1807)": _mm(1000, 1800, 700),
+    "matmul 1024^3, B column-major": _mm(1024, 1024, 1024),
     "softmax 4096 x 1024": (2 * 4 * 4096 * 1024, None),
     "softmax 4096 x 4096": (2 * 4 * 4096 * 4096, None),
     "softmax 4096 x 1823": (2 * 4 * 4096 * 1823, None),
     "attention 32 x 1024 x 64 causal": (4 * 32 * 1024 * 64 * 4, 4 * 1024 * 1024 * 64 * 32 // 2),
+    "digits MLP, 1797 images": (_MLP_BYTES, _MLP_FLOPS),
 }
 # their launches, identified by kernel name and Grid_Size_X (work-items), with the number of
-# times a step runs each (the 4096^3 matmul: two launches of 256 tiles of 128 x 256, one per CU)
+# times a step runs each (the 4096^3 matmul: two launches of 256 tiles of 128 x 256, one per CU;
+# the split GEMM's template arguments are <row blocks, column blocks, waves splitting K, A's
+# layout (0: rows 16-byte aligned, 1: unaligned rows), B column-major>)
 LAUNCHES = {
     ("gemm_direct_kernel<true, true, false, 4>", 65536): ("matmul 4096^3", 2),
+    ("gemm_split_kernel<1, 1, 4, 0, false>", 65536): ("matmul 512^3", 1),
+    ("gemm_split_kernel<2, 2, 4, 0, false>", 65536): ("matmul 1024^3", 1),
+    ("gemm_split_kernel<2, 2, 4, 1, false>", 118784): ("matmul 1000 x 1800 x 700 (row strides 703 / 1805 / 1807)", 1),
+    ("gemm_split_kernel<2, 2, 4, 0, true>", 65536): ("matmul 1024^3, B column-major", 1),
     ("softmax_rows_kernel<4, true>", 262144): ("softmax 4096 x 1024", 1),
     ("softmax_wg_kernel<2, 512, true>", 2097152): ("softmax 4096 x 4096", 1),
     ("softmax_rows_kernel<8, false>", 196608): ("softmax 4096 x 1823", 1),
     ("attn_fwd_fast<64, true>", 131072): ("attention 32 x 1024 x 64 causal", 1),
+    ("mlp3_rows16_kernel<64, 128, 64, 10>", 28928): ("digits MLP, 1797 images", 1),
 }
+MAX_CLOCK_GHZ = 2.4  # the engine clock's maximum: a lower bound on busy cycles per busy time
 TIMED = "matmul 4096^3"  # the workload of bench.py's timed region
 
 
@@ -139,28 +161,60 @@ def summarize(kt_dir, fetch_dir, write_dir, timed_steps=0):
 
 def mfma_busy(pmc_dir, xcds=8, simds=1024):
     """MFMA pipe occupancy per benchmark MFMA workload from a
-    `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES` run: SQ_VALU_MFMA_BUSY_CYCLES is summed
-    over the SIMDs and GRBM_GUI_ACTIVE over the XCDs (both as rocprofv3 reports them), so
-    busy = MFMA cycles / (GUI cycles / xcds * simds), a ratio of cycles that does not depend
-    on the clock the kernel ran at; over all dispatches of a workload's launches (weighted by
-    their cycles)."""
+    `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES` run, in two normalisations (summed over all
+    dispatches of a workload's launches):
+      * per GUI cycle: SQ_VALU_MFMA_BUSY_CYCLES (summed over the SIMDs) / (GRBM_GUI_ACTIVE / xcds *
+        simds). GRBM_GUI_ACTIVE counts every cycle of the counter window, which under the
+        profiler is longer than the kernel (the dispatch and its drain), so this understates the
+        kernel's own occupancy, most for short launches;
+      * per kernel cycle: the same busy cycles / (simds * the dispatch's own duration, End_Timestamp -
+        Start_Timestamp, * MAX_CLOCK_GHZ): the occupancy over the kernel's span at the maximum
+        clock (a lower bound: the clock is at most that).
+    `window_over_kernel` is the ratio of the two denominators."""
     per = {}
     for r in csv.DictReader(open(_one(os.path.join(pmc_dir, "*_counter_collection.csv")))):
         key = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
         if key not in LAUNCHES or not WORKLOADS[LAUNCHES[key][0]][1]:
             continue
-        per.setdefault((key, r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+        d = per.setdefault((key, r["Dispatch_Id"]), {})
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+        d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
     out = {}
     for (key, _), d in per.items():
         if "GRBM_GUI_ACTIVE" in d and "SQ_VALU_MFMA_BUSY_CYCLES" in d:
-            w = out.setdefault(LAUNCHES[key][0], dict(kernels=[], dispatches=0, busy=0.0, cycles=0.0))
+            w = out.setdefault(LAUNCHES[key][0], dict(kernels=[], dispatches=0, busy=0.0, cycles=0.0, kcycles=0.0,
+                                                      ns=0))
             if key[0] not in w["kernels"]:
                 w["kernels"].append(key[0])
             w["dispatches"] += 1
             w["busy"] += d["SQ_VALU_MFMA_BUSY_CYCLES"]
             w["cycles"] += d["GRBM_GUI_ACTIVE"] / xcds * simds
-    return {label: dict(kernel=" + ".join(w["kernels"]), dispatches=w["dispatches"], mfma_busy=w["busy"] / w["cycles"])
+            w["kcycles"] += d["ns"] * MAX_CLOCK_GHZ * simds
+            w["ns"] += d["ns"]
+    return {label: dict(kernel=" + ".join(w["kernels"]), dispatches=w["dispatches"], mfma_busy=w["busy"] / w["cycles"],
+                        mfma_busy_kernel=w["busy"] / w["kcycles"], kernel_us=w["ns"] / w["dispatches"] / 1e3,
+                        window_over_kernel=w["cycles"] / w["kcycles"],
+                        busy_cycles_per_launch=w["busy"] / w["dispatches"])
             for label, w in out.items()}
+
+
+def mfma_busy_traced(pmc_dir, kt_dir, clock_ghz, simds=1024):
+    """The busy cycles of each MFMA workload's launch (a count of the work: MFMAs x their cycles,
+    the same with or without the profiler) over the cycles of its median span in a kernel trace
+    (where the kernels run as in the benchmark; under --pmc they run slower) at `clock_ghz`, the
+    clock the device sustains (bench.py's mfma_sustained)."""
+    spans = {}
+    for r in kernel_stats(kt_dir):
+        key = (r["kernel"], r["grid"])
+        if key in LAUNCHES:
+            spans[LAUNCHES[key][0]] = (r["median_ns"], LAUNCHES[key][1])
+    out = {}
+    for label, m in mfma_busy(pmc_dir, simds=simds).items():
+        if label in spans:
+            ns, per_step = spans[label]
+            out[label] = dict(m, traced_median_us=ns / 1e3,
+                              mfma_busy_traced=m["busy_cycles_per_launch"] / (simds * ns * clock_ghz))
+    return out
 
 
 def _per_dispatch(pmc_dir):
@@ -212,6 +266,10 @@ def main(argv=None):
     ap.add_argument("--commit", default=None, help="the commit the traced runs were made at (recorded)")
     ap.add_argument("--mfma", action="store_true",
                     help="kt_dir is a --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES run: print MFMA occupancy")
+    ap.add_argument("--trace", default=None,
+                    help="with --mfma: a --kernel-trace run of bench.py, whose median spans normalise the busy cycles")
+    ap.add_argument("--clock", type=float, default=MAX_CLOCK_GHZ,
+                    help="with --trace: the engine clock in GHz (bench.py's mfma_sustained clock_ghz)")
     ap.add_argument("--lds", action="store_true",
                     help="kt_dir is a --pmc GRBM_GUI_ACTIVE SQ_WAVE_CYCLES SQ_LDS_IDX_ACTIVE SQ_LDS_BANK_CONFLICT run: "
                          "print resident waves and LDS bank conflicts")
@@ -226,9 +284,19 @@ def main(argv=None):
                              f"{m['lds_active']:.3g} | {m['lds_conflict_cycles']:.3g} | {ratio} |\n")
         return
     if a.mfma:
-        sys.stdout.write("| workload | kernel | dispatches | MFMA pipe busy |\n|---|---|---|---|\n")
+        traced = mfma_busy_traced(a.kt_dir, a.trace, a.clock) if a.trace else {}
+        sys.stdout.write("| workload | kernel | dispatches | busy cycles per launch | kernel us under --pmc | "
+                         f"busy per cycle of that span (at {MAX_CLOCK_GHZ} GHz) | busy per GUI cycle | "
+                         "counter window / span |" + (f" traced median us | busy per cycle of the traced span "
+                                                      f"(at {a.clock} GHz) |" if traced else "") + "\n" +
+                         "|---" * (8 + (2 if traced else 0)) + "|\n")
         for label, m in mfma_busy(a.kt_dir).items():
-            sys.stdout.write(f"| {label} | `{m['kernel']}` | {m['dispatches']} | {100 * m['mfma_busy']:.1f} % |\n")
+            t = traced.get(label)
+            sys.stdout.write(f"| {label} | `{m['kernel']}` | {m['dispatches']} | {m['busy_cycles_per_launch']:.4g} | "
+                             f"{m['kernel_us']:.2f} | {100 * m['mfma_busy_kernel']:.1f} % | "
+                             f"{100 * m['mfma_busy']:.1f} % | {m['window_over_kernel']:.2f} |" +
+                             (f" {t['traced_median_us']:.2f} | {100 * t['mfma_busy_traced']:.1f} % |" if t else
+                              (" — | — |" if traced else "")) + "\n")
         return
     stats, traffic, ff, fw = summarize(a.kt_dir, a.fetch_dir, a.write_dir, a.timed_steps)
     steps = workload_steps(stats)
@@ -242,11 +310,20 @@ def main(argv=None):
                   f"take {t['timed_step_ns'] / 1e3:.2f} us per step together = "
                   f"{t['flops'] / t['timed_step_ns'] / 1e3:.1f} TFLOP/s.\n\n")
     out.write("## Benchmark workloads (kernel time per step: the averages of the step's launches, summed)\n\n")
-    out.write("| workload | launches per step | us per step | achieved |\n|---|---|---|---|\n")
+    out.write("The 4096^3 row leads with bench.py's timed steps (the dispatches of its timed region); every row "
+              "also gives the average over all of the workload's dispatches (warm-up, clock ramp and the "
+              "HIP-graph replays included).\n\n")
+    out.write("| workload | launches per step | us per step (timed steps) | achieved (timed steps) | "
+              "us per step (all dispatches) | achieved (all dispatches) |\n|---|---|---|---|---|---|\n")
+
+    def achieved(w, ns):
+        return (f"{w['flops'] / ns / 1e3:.1f} TFLOP/s" if w["flops"] else f"{w['algorithmic_bytes'] / ns:.0f} GB/s")
+
     for label, w in steps.items():
-        ach = (f"{w['flops'] / w['step_ns'] / 1e3:.1f} TFLOP/s" if w["flops"]
-               else f"{w['algorithmic_bytes'] / w['step_ns']:.0f} GB/s")
-        out.write(f"| {label} | {' + '.join(f'`{k}`' for k in w['launches'])} | {w['step_ns'] / 1e3:.2f} | {ach} |\n")
+        timed = (f"{w['timed_step_ns'] / 1e3:.2f} | {achieved(w, w['timed_step_ns'])}" if "timed_step_ns" in w
+                 else "— | —")
+        out.write(f"| {label} | {' + '.join(f'`{k}`' for k in w['launches'])} | {timed} | "
+                  f"{w['step_ns'] / 1e3:.2f} | {achieved(w, w['step_ns'])} |\n")
     out.write("\n## Kernel durations (rocprofv3 --kernel-trace, per dispatch, grouped by grid)\n\n")
     out.write("| kernel | grid (work-items) | benchmark workload | calls | avg us | median us | min us | max us |\n"
               "|---|---|---|---|---|---|---|---|\n")

@@ -87,3 +87,20 @@ def test_lds_occupancy(tmp_path):
     assert a["kernel"] == "attn_fwd_fast<64, true>" and a["dispatches"] == 1
     assert a["waves_per_simd"] == pytest.approx(2.0)
     assert a["lds_conflict_ratio"] == pytest.approx(0.5)
+
+
+def test_mfma_busy_per_kernel_cycle_against_a_longer_counter_window(tmp_path):
+    """The counter window (GRBM_GUI_ACTIVE) of the second dispatch is 1.25 times its own span:
+    per GUI cycle the two dispatches are 2.88 / 3.9 busy, per kernel cycle at 2.4 GHz 0.8."""
+    d = str(tmp_path / "pmc")
+    gui, gui2 = 8 * 2.4e6, 8 * 1.5e6
+    busy, busy2 = 0.9 * 2.4e6 * 1024, 0.6 * 1.2e6 * 1024
+    write_pmc(d, [(7, GEMM, 65536, "GRBM_GUI_ACTIVE", gui, 5_000, 1_005_000),
+                  (7, GEMM, 65536, "SQ_VALU_MFMA_BUSY_CYCLES", busy, 5_000, 1_005_000),
+                  (8, GEMM, 65536, "GRBM_GUI_ACTIVE", gui2, 1_005_000, 1_505_000),
+                  (8, GEMM, 65536, "SQ_VALU_MFMA_BUSY_CYCLES", busy2, 1_005_000, 1_505_000)])
+    m = profiling.mfma_busy(d)["matmul 4096^3"]
+    assert m["mfma_busy"] == pytest.approx(2.88 / 3.9)
+    assert m["mfma_busy_kernel"] == pytest.approx(0.8)
+    assert m["window_over_kernel"] == pytest.approx(3.9 / 3.6)
+    assert m["kernel_us"] == pytest.approx(750.0)

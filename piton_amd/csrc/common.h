@@ -124,6 +124,15 @@ __device__ __forceinline__ T sgpr_keep(T v) {
     return v;
 }
 
+// a < b ? x : 0 for wave-uniform values, as a scalar compare and select. Written out so that
+// the compiler cannot turn it into a branch: one inside a loop whose accumulators live in AGPRs
+// makes it copy them to VGPRs and back each iteration.
+__device__ __forceinline__ int scalar_lt_select(int a, int b, int x) {
+    int r;
+    asm("s_cmp_lt_i32 %1, %2\n\ts_cselect_b32 %0, %3, 0" : "=s"(r) : "s"(a), "s"(b), "s"(x) : "scc");
+    return r;
+}
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 // a * b and a + b for the host's size checks on caller-supplied extents and strides: INT64_MAX

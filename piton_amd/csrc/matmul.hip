@@ -561,7 +561,7 @@ void gemm_direct_kernel(GemmArgs g) {
 constexpr int kMaxSplitWaves = PITON_SPLIT_MAX_WAVES;
 enum SplitA { A_ROW16 = 0, A_ROW = 1, A_COL = 2 };
 
-template <int NB, int NBN, int KS, int AM, bool BKC>
+template <int NB, int NBN, int KS, int AM, bool BKC, bool TAIL>
 __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     constexpr bool AVEC = AM == A_ROW16;
     constexpr int TB = 32 * NB, TBN = 32 * NBN;  // tile rows and columns
@@ -597,10 +597,8 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     const int off0 = AM == A_COL ? 0 : (int)((reinterpret_cast<uintptr_t>(g.a) >> 2) & 3);  // A's first float past the boundary
     const float *a_al = g.a - off0;
     const int64_t a_end = off0 + (g.M - 1) * s_am + (g.K - 1) * s_ak + 1;  // floats from a_al
-    const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a_al), (short)0,
-                                                      (int)(((a_end + 3) & ~(int64_t)3) * 4), 0x00020000);
-    const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(g.b), (short)0,
-                                                      (int)(((g.K - 1) * s_bk + (g.N - 1) * s_bn + 1) * 4), 0x00020000);
+    const int64_t a_bound = ((a_end + 3) & ~(int64_t)3) * 4;                              // bytes
+    const int64_t b_bound = ((g.K - 1) * s_bk + (g.N - 1) * s_bn + 1) * 4;
     uint32_t va[NB], vb[NBN];
     int ra_shift[NB];  // A_ROW: this lane's row start past its 16-byte boundary, in floats
 #pragma unroll
@@ -613,21 +611,47 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     for (int j = 0; j < NBN; j++) vb[j] = (uint32_t)(((int64_t)(16 * half) * s_bk + (n0 + j * 32 + l31) * s_bn) * 4);
     const uint32_t sak4 = (uint32_t)(s_ak * 4), sbk4 = (uint32_t)(s_bk * 4);
     const int nk = (int)((g.K + 31) / 32);
+    // per-lane offsets that do not change from tile to tile: one float per k of a column-major A
+    // (va[i] is va[0] + 128 i) and of a row-major B (vb[j] is vb[0] + 128 j): the block offsets
+    // go in the instructions' immediate offsets
+    uint32_t vas[AM == A_COL ? 16 : 1], vbs[BKC ? 1 : 16];
+    if constexpr (AM == A_COL) {
+#pragma unroll
+        for (int s = 0; s < 16; s++) vas[s] = va[0] + s * sak4;
+    }
+    if constexpr (!BKC) {
+#pragma unroll
+        for (int s = 0; s < 16; s++) vbs[s] = vb[0] + s * sbk4;
+    }
 
     constexpr int AW = AM == A_ROW ? 20 : 16;  // A floats a lane loads per block and tile
     struct Ops {
         float a[NB][AW];
         float b[NBN][16];
     };
-    // every offset goes in the per-lane address, which is what the descriptor's range check
-    // covers. The K tail: a row-major A's elements and a column-major B's with k >= K get an
-    // offset past the bound (2^31, beyond any bound of a matrix under 2 GiB), so they read as zero
-    // with no data dependence; a column-major A's and a row-major B's lie past the bound already.
+    // A tile's loads go through descriptors whose base is advanced to the tile and whose bound
+    // shrinks by as much (scalar arithmetic only: with K % 32 == 0 the loop has no vector address
+    // arithmetic), so the range check, which covers the per-lane offset, still ends each at its
+    // matrix's last element: offsets at or past it read as zero. Tiles past the last one (a wave's
+    // K tiles come in pairs) read through a bound of 0: zeros. TAIL (K % 32 != 0), inside the
+    // last tile, k >= K: a column-major A's and a row-major B's elements lie past the bound; a
+    // row-major A's 16-byte chunks and a column-major B's get an offset past the bound (2^31) by a
+    // select against the tile's remaining k (a compare and a select per chunk, no branch: control
+    // flow in the loop makes the compiler copy the accumulators out of AGPRs each iteration).
     constexpr uint32_t kOut = 0x80000000u;
+    auto rsrc = [&](const float *base, int64_t bound, uint32_t step4, int kt) {
+        const int64_t shift = (int64_t)kt * 32 * step4;  // past the last tile the base is never read
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(reinterpret_cast<const char *>(base) + shift),
+                                                 (short)0, scalar_lt_select(kt, nk, (int)(bound - shift)),
+                                                 0x00020000);
+    };
     // PIN keeps the loads in source order with scheduling barriers (A first, then B step by step).
     auto load = [&](int kt, Ops &o, auto pin) {
-        const uint32_t ka = (uint32_t)kt * 32u * sak4, kb = (uint32_t)kt * 32u * sbk4;
-        const int64_t k0 = (int64_t)kt * 32 + 16 * half;  // this lane's first k of the tile
+        const auto ra = rsrc(a_al, a_bound, sak4, kt);
+        const auto rb = rsrc(g.b, b_bound, sbk4, kt);
+        const int rem = (int)(g.K - (int64_t)kt * 32) - 16 * half;  // TAIL: this lane's k below K in the tile
+        // TAIL: the offset of a chunk of four k starting c past the lane's first k of the tile
+        auto chunk = [&](uint32_t off, int c) -> int { return (int)(!TAIL || c < rem ? off : kOut); };
         auto pinned = [&]() {
             if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
         };
@@ -638,24 +662,15 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
                 // lies at or past (K - 1) s_ak + M, the bound
 #pragma unroll
                 for (int s = 0; s < 16; s++) {
-                    o.a[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)(va[i] + ka + s * sak4), 0, 0));
-                    pinned();
-                }
-            } else if constexpr (AVEC) {
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t off = k0 + 4 * q < g.K ? va[i] + ka + 16 * q : kOut;
-                    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0));
-#pragma unroll
-                    for (int e = 0; e < 4; e++) o.a[i][4 * q + e] = v[e];
+                    o.a[i][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, (int)(vas[s] + 128 * i), 0, 0));
                     pinned();
                 }
             } else {
-                // the chunks holding k0 - r .. k0 - r + 19; the K tail is zeroed in mul
+                // A_ROW16: four chunks of four k; A_ROW: the five chunks holding k0 - r .. k0 - r + 19
 #pragma unroll
-                for (int q = 0; q < 5; q++) {
-                    const uint32_t off = k0 - ra_shift[i] + 4 * q < g.K ? va[i] + ka + 16 * q : kOut;
-                    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0));
+                for (int q = 0; q < (AVEC ? 4 : 5); q++) {
+                    const int off = AVEC ? chunk(va[i] + 16 * q, 4 * q) : (int)(va[i] + 16 * q);
+                    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
 #pragma unroll
                     for (int e = 0; e < 4; e++) o.a[i][4 * q + e] = v[e];
                     pinned();
@@ -667,8 +682,8 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
             for (int j = 0; j < NBN; j++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const uint32_t off = k0 + 4 * q < g.K ? vb[j] + kb + 16 * q : kOut;
-                    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0));
+                    const f32x4 v =
+                        __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, chunk(vb[j] + 16 * q, 4 * q), 0, 0));
 #pragma unroll
                     for (int e = 0; e < 4; e++) o.b[j][4 * q + e] = v[e];
                     pinned();
@@ -678,7 +693,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
             for (int s = 0; s < 16; s++)
 #pragma unroll
                 for (int j = 0; j < NBN; j++) {
-                    o.b[j][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)(vb[j] + kb + s * sbk4), 0, 0));
+                    o.b[j][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (int)(vbs[s] + 128 * j), 0, 0));
                     pinned();
                 }
         }
@@ -1090,20 +1105,24 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     return p;
 }
 
-// the recorded name of gemm_split_kernel<NB, NBN, KS, AM, BKC>, with its parameters' values
-template <int NB, int NBN, int KS, int AM, bool BKC>
+// the recorded name of gemm_split_kernel<NB, NBN, KS, AM, BKC, TAIL>, with its parameters' values
+template <int NB, int NBN, int KS, int AM, bool BKC, bool TAIL>
 static const char *split_name() {
     static const std::string name = "gemm_split_kernel<" + std::to_string(NB) + ", " + std::to_string(NBN) + ", " +
                                     std::to_string(KS) + ", " +
                                     (AM == A_ROW16 ? "A_ROW16" : AM == A_ROW ? "A_ROW" : "A_COL") + ", " +
-                                    (BKC ? "true" : "false") + ">";
+                                    (BKC ? "true" : "false") + ", " + (TAIL ? "true" : "false") + ">";
     return name.c_str();
 }
 
 template <int NB, int NBN, int KS, int AM, bool BKC>
 static void launch_split_one(const GemmArgs &g, unsigned nwg, hipStream_t st) {
-    PITON_LAUNCH_NAMED((gemm_split_kernel<NB, NBN, KS, AM, BKC>), (split_name<NB, NBN, KS, AM, BKC>()), dim3(nwg),
-                       dim3(64 * KS), 0, st, g);
+    if (g.K % 32 == 0)
+        PITON_LAUNCH_NAMED((gemm_split_kernel<NB, NBN, KS, AM, BKC, false>), (split_name<NB, NBN, KS, AM, BKC, false>()),
+                           dim3(nwg), dim3(64 * KS), 0, st, g);
+    else
+        PITON_LAUNCH_NAMED((gemm_split_kernel<NB, NBN, KS, AM, BKC, true>), (split_name<NB, NBN, KS, AM, BKC, true>()),
+                           dim3(nwg), dim3(64 * KS), 0, st, g);
 }
 
 template <int NB, int NBN, int KS>

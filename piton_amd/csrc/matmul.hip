@@ -758,22 +758,32 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
 #ifndef PITON_SPLIT_LPM
 #define PITON_SPLIT_LPM 1
 #endif
+
     // 32 x 32 tiles (NB = 1): 20 loads against 16 MFMAs, two after each so that every load is in
     // flight before the tile's last product (512^3: 6.04 -> 5.72 us; 64 x 64 tiles keep one:
     // 1024^3 20.9 against 21.7 us with two, 22.4 with three)
     constexpr int LOADS = NB * (AM == A_ROW16 ? 4 : AM == A_ROW ? 5 : 16) + NBN * (BKC ? 4 : 16);
     constexpr int MFMAS = 16 * NB * NBN, LPM = NB == 1 ? 2 : PITON_SPLIT_LPM;
+    // PRECISE: each product waits only for its own operands (the compiler's counts) instead of
+    // the whole tile at each half's start, and the next tile's loads go out from product
+    // LOAD_START on. Measured per layout: faster on 32 x 32 tiles (512^3 5.46 -> 5.30 us, 768^2
+    // x 2048 32.1 -> 30.8) and, loads from the 17th product on, on 64 x 64 tiles with B
+    // column-major (1024^3 20.7 -> 20.1); slower on 64 x 64 tiles with B row-major (1024^3 19.6
+    // -> 20.8, 1024^2 x 4096 61.9 -> 68.1).
+    constexpr bool PRECISE = NB == 1 || BKC;
+    constexpr int LOAD_START = NB == 2 && BKC ? 16 : 0;
     auto interleave = [&]() {
 #pragma unroll
         for (int i = 0; i < MFMAS; i++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            if (i * LPM < LOADS) __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);  // LPM VMEM reads
+            if (i >= LOAD_START && (i - LOAD_START) * LPM < LOADS)
+                __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);  // LPM VMEM reads
         }
     };
-    // Each half starts with every load of its tile landed (vmcnt(0)): its tile's loads went out
-    // during the other half, and waiting only for the first of them would let the next tile's
-    // loads join them, 80 in flight against the 63 a wave's vector-memory counter tracks, which
-    // stalls the issue of loads and products alike (1024^2 x 4096: 69.0 -> 77.7 us).
+    // Without PRECISE each half starts with every load of its tile landed (vmcnt(0)): its tile's
+    // loads went out during the other half. With PRECISE the prologue's loads land before the
+    // loop (else the compiler's counts at the loop head merge the prologue's load order with the
+    // loop's and wait for nearly all of them) and each product then waits for its own operands.
     // The prologue's loads go out in source order on 32 x 32 tiles (a wave has few K tiles, and
     // the first products start when their operands arrive: 512^3 5.72 -> 5.6 us); on 64 x 64
     // tiles that order measured slower in the loop that follows (1024^2 x 4096: 77 against 69 us,
@@ -781,16 +791,17 @@ __global__ __launch_bounds__(64 * KS) void gemm_split_kernel(GemmArgs g) {
     Ops o0, o1;
     if constexpr (NB == 1) load(wave, o0, Pin());
     else load(wave, o0, Free());
+    if constexpr (PRECISE) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     PITON_PHASE_WAIT_LOADS();
     PITON_PHASE(1);
     for (int kt = wave; kt < nk; kt += 2 * KS) {
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        if constexpr (!PRECISE) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
         __builtin_amdgcn_sched_barrier(0);
         load(kt + KS, o1, Free());
         mul(o0, kt);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        if constexpr (!PRECISE) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
         __builtin_amdgcn_sched_barrier(0);
         load(kt + 2 * KS, o0, Free());
         mul(o1, kt + KS);
@@ -1082,7 +1093,10 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     const int nb = PITON_SPLIT_NB_MAX > 1 && tiles(64) >= cus ? 2 : 1;
     const int64_t nt = tiles(32 * nb);
     int ks = 1;
-    while (ks < kMaxSplitWaves && nt * ks < PITON_SPLIT_WAVES_PER_CU * (int64_t)cus && 4 * ks <= nk) ks *= 2;
+    // (eight waves only on 64 x 64 tiles: their reduction gives each wave two groups of four
+    // accumulators; a 32 x 32 tile has four groups)
+    const int ks_max = nb == 2 ? kMaxSplitWaves : min(kMaxSplitWaves, 4);
+    while (ks < ks_max && nt * ks < PITON_SPLIT_WAVES_PER_CU * (int64_t)cus && 4 * ks <= nk) ks *= 2;
     // every byte offset a lane forms (the prefetch past the last tile included) stays below 2^31
     const int64_t tb = 32 * nb, kpad = g.K + 32 * (2 * ks + 3);  // the farthest prefetch: tile nk - 1 + 2 ks
     if (sat_add(sat_mul(g.M + tb, g.s_am), sat_mul(kpad, g.s_ak)) >= (1LL << 29) - 4 ||
@@ -1094,10 +1108,10 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     // splitting K give each SIMD one wave with the same MFMA work as two waves of the square
     // tile, and the wave's 2 x 4 blocks need 0.56 loads per product instead of 0.63
     const int64_t ntw = tiles2(64, 128);
-    // (measured where A's rows are 16-byte aligned and B is row-major: 2048 x 768 x 256 15.9 ->
-    // 15.4 us, 1024 x 2048 x 256 16.3 -> 15.8; the same on the aligned ragged shape; 2-3 % slower
-    // with A's rows unaligned or B column-major, which keep the square tile)
-    if (nb == 2 && ks == 4 && nt > cus && ntw <= cus && p.am == A_ROW16 && !p.bkc && PITON_SPLIT_WIDE &&
+    // (measured with B row-major: 2048 x 768 x 256 15.9 -> 15.4 us, 1024 x 2048 x 256 16.3 ->
+    // 15.8; the same on the ragged shape with 16-byte aligned rows, 33.0 -> 32.2 with A's row
+    // stride 703; B column-major measured slower and keeps the square tile)
+    if (nb == 2 && ks == 4 && nt > cus && ntw <= cus && p.am != A_COL && !p.bkc && PITON_SPLIT_WIDE &&
         sat_add(sat_mul(kpad, g.s_bk), sat_mul(g.N + 128, g.s_bn)) < (1LL << 29)) {
         p.nbn = 4;
         p.tiles = ntw;
@@ -1140,7 +1154,7 @@ static void launch_split_nb(const GemmArgs &g, const SplitPlan &sp, unsigned nwg
     if (sp.ks == 1) launch_split_ks<NB, NB, 1>(g, sp.am, sp.bkc, nwg, st);
     else if (sp.ks == 2) launch_split_ks<NB, NB, 2>(g, sp.am, sp.bkc, nwg, st);
 #if PITON_SPLIT_MAX_WAVES > 4
-    else if (sp.ks == 8) launch_split_ks<NB, NB, 8>(g, sp.am, sp.bkc, nwg, st);
+    else if (NB == 2 && sp.ks == 8) launch_split_ks<2, 2, 8>(g, sp.am, sp.bkc, nwg, st);
 #endif
     else if (NB == 2 && sp.nbn == 4) launch_split_ks<2, 4, 4>(g, sp.am, sp.bkc, nwg, st);
     else launch_split_ks<NB, NB, 4>(g, sp.am, sp.bkc, nwg, st);

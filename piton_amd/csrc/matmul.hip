@@ -906,7 +906,7 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 // 16-byte-aligned row (per lane (x0 + x1) + (x2 + x3) over its float4 chunks, DPP wave sums,
 // a second pass of fmaf squares): the product sees the very values the separate layernorm
 // would have written. Needs the FAST layout.
-template <bool FAST, bool LN>
+template <bool FAST, bool LN, int KQ = 0>
 __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) {
     keep_epilogue_args(g);
     static_assert(!LN || FAST, "LN needs the FAST layout");
@@ -921,14 +921,18 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
     const int64_t m = m0 + c16;  // the A row this lane supplies
     const bool m_ok = m < g.M;
     f32x4v acc = f32x4v{0.f, 0.f, 0.f, 0.f};
-    // the epilogue's bias and residual, requested now: thread (r, lane) = (t / 64, t % 64) < 256
-    // finishes output (m0 + 4*grp + r, n), and only it reads and writes that element (so a
-    // residual that is the output itself is read before it is written)
+    // the epilogue's bias and residual, requested with the operands (epilogue_loads): thread
+    // (r, lane) = (t / 64, t % 64) < 256 finishes output (m0 + 4*grp + r, n), and only it reads
+    // and writes that element (so a residual that is the output itself is read before it is
+    // written)
     const int er = t >> 6;
     const int64_t emo = m0 + 4 * grp + er;
     const bool e_ok = t < 256 && emo < g.M && n_ok;
-    const float e_bias = (e_ok && g.bias) ? g.bias[n] : 0.f;
-    const float e_res = (e_ok && g.res) ? g.res[emo * g.s_rm + n] : 0.f;
+    float e_bias = 0.f, e_res = 0.f;
+    auto epilogue_loads = [&]() {
+        e_bias = (e_ok && g.bias) ? g.bias[n] : 0.f;
+        e_res = (e_ok && g.res) ? g.res[emo * g.s_rm + n] : 0.f;
+    };
     float ln_mean = 0.f, ln_inv = 1.f;
     // LN: wave w computes the statistics of row m0 + w (K % 256 == 0, so a lane's chunks are
     // lane + 64c); a row of up to 1024 columns stays in registers for the variance pass
@@ -1008,20 +1012,40 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
 #pragma unroll
             for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], wb[j], acc, 0, 0, 0);
         };
-        f32x4v xa0, xa1;
-        float wb0[4], wb1[4];
-        load(0, xa0, wb0);  // in flight while the LN statistics are computed
-        if constexpr (LN) ln_stats();
-        for (int64_t s = 0; s < kq; s += 8) {
-            if (s + 4 < kq) load(s + 4, xa1, wb1);
-            ready(xa0);
-            mul(xa0, wb0);
-            if (s + 4 >= kq) break;
-            if (s + 8 < kq) load(s + 8, xa0, wb0);
-            ready(xa1);
-            mul(xa1, wb1);
+        if constexpr (KQ > 0) {
+            // K = 64 KQ: the lane group's whole k range is requested at once, one memory round
+            // trip, and the bias and residual after it (a wait for these covers them all)
+            f32x4v xa[KQ / 4];
+            float wb[KQ / 4][4];
+#pragma unroll
+            for (int c = 0; c < KQ / 4; c++) load(4 * c, xa[c], wb[c]);
+            __builtin_amdgcn_sched_barrier(0);
+            epilogue_loads();
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (LN) ln_stats();
+#pragma unroll
+            for (int c = 0; c < KQ / 4; c++) {
+                ready(xa[c]);
+                mul(xa[c], wb[c]);
+            }
+        } else {
+            epilogue_loads();
+            f32x4v xa0, xa1;
+            float wb0[4], wb1[4];
+            load(0, xa0, wb0);  // in flight while the LN statistics are computed
+            if constexpr (LN) ln_stats();
+            for (int64_t s = 0; s < kq; s += 8) {
+                if (s + 4 < kq) load(s + 4, xa1, wb1);
+                ready(xa0);
+                mul(xa0, wb0);
+                if (s + 4 >= kq) break;
+                if (s + 8 < kq) load(s + 8, xa0, wb0);
+                ready(xa1);
+                mul(xa1, wb1);
+            }
         }
     } else {
+        epilogue_loads();
         const float *wp = g.b + n;
         for (int64_t s = 0; s < kq; s++) {
             const int64_t k = kbeg + s;
@@ -1047,6 +1071,24 @@ __global__ __launch_bounds__(64 * SMWAVES) void gemm_small_m_kernel(GemmArgs g) 
     if (g.relu && v < 0.f) v = 0.f;  // NaN passes, as np.maximum(NaN, 0)
     if (g.res) v += e_res;
     g.c[mo * g.s_cm + n] = v;
+}
+
+// the FAST small-M kernel, with the whole K range of a lane group loaded at once where K is
+// 256, 512 or 1024 (the decoder's products: 1024 in one round trip instead of two)
+template <bool LN>
+static void launch_small_m(const GemmArgs &g, dim3 grid, dim3 block, hipStream_t st) {
+    const int64_t kq = g.K / (4 * SMWAVES);
+    auto name = [](int q) {
+        static const char *n[2][4] = {{"gemm_small_m_kernel<true, false, 0>", "gemm_small_m_kernel<true, false, 4>",
+                                       "gemm_small_m_kernel<true, false, 8>", "gemm_small_m_kernel<true, false, 16>"},
+                                      {"gemm_small_m_kernel<true, true, 0>", "gemm_small_m_kernel<true, true, 4>",
+                                       "gemm_small_m_kernel<true, true, 8>", "gemm_small_m_kernel<true, true, 16>"}};
+        return n[LN ? 1 : 0][q];
+    };
+    if (kq == 4) PITON_LAUNCH_NAMED((gemm_small_m_kernel<true, LN, 4>), name(1), grid, block, 0, st, g);
+    else if (kq == 8) PITON_LAUNCH_NAMED((gemm_small_m_kernel<true, LN, 8>), name(2), grid, block, 0, st, g);
+    else if (kq == 16) PITON_LAUNCH_NAMED((gemm_small_m_kernel<true, LN, 16>), name(3), grid, block, 0, st, g);
+    else PITON_LAUNCH_NAMED((gemm_small_m_kernel<true, LN, 0>), name(0), grid, block, 0, st, g);
 }
 
 static int layout_a(const GemmArgs &g) {
@@ -1331,7 +1373,7 @@ int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *w, const f
         PITON_REQUIRE((N + SMN - 1) / SMN <= 0x7FFFFFFF, PITON_EUNSUPPORTED, "linear: N=%lld too large", (long long)N);
         const dim3 grid((unsigned)((N + SMN - 1) / SMN), (unsigned)((M + 15) / 16)), block(64 * SMWAVES);
         if (K % (16 * SMWAVES) == 0 && ldx % 4 == 0 && aligned16(x))
-            PITON_LAUNCH((gemm_small_m_kernel<true, false>), grid, block, 0, (hipStream_t)stream, g);
+            launch_small_m<false>(g, grid, block, (hipStream_t)stream);
         else
             PITON_LAUNCH((gemm_small_m_kernel<false, false>), grid, block, 0, (hipStream_t)stream, g);
         rc = check_launch("linear");
@@ -1363,7 +1405,7 @@ int32_t piton_mi355x_linear_ln(const float *x, int64_t ldx, float eps, const flo
     if (M == 0) return PITON_OK;
     GemmArgs g{x, w, y, M, N, K, ldx, 1, N, 1, ldy, 1, 1, bias, relu ? 1 : 0, residual, ldr, 0, 0, eps};
     const dim3 grid((unsigned)((N + SMN - 1) / SMN), (unsigned)((M + 15) / 16)), block(64 * SMWAVES);
-    PITON_LAUNCH((gemm_small_m_kernel<true, true>), grid, block, 0, (hipStream_t)stream, g);
+    launch_small_m<true>(g, grid, block, (hipStream_t)stream);
     rc = check_launch("linear_ln");
     if (rc == PITON_OK) clear_error();
     return rc;

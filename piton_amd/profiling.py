@@ -54,12 +54,13 @@ WORKLOADS = {
 # their launches, identified by kernel name and Grid_Size_X (work-items), with the number of
 # times a step runs each (the 4096^3 matmul: two launches of 256 tiles of 128 x 256, one per CU;
 # the split GEMM's template arguments are <row blocks, column blocks, waves splitting K, A's
-# layout (0: rows 16-byte aligned, 1: unaligned rows), B column-major>)
+# layout (0: rows 16-byte aligned, 1: unaligned rows), B column-major, K % 32 != 0>; the ragged
+# shape runs 240 wide tiles of 64 x 128)
 LAUNCHES = {
     ("gemm_direct_kernel<true, true, false, 4>", 65536): ("matmul 4096^3", 2),
     ("gemm_split_kernel<1, 1, 4, 0, false, false>", 65536): ("matmul 512^3", 1),
     ("gemm_split_kernel<2, 2, 4, 0, false, false>", 65536): ("matmul 1024^3", 1),
-    ("gemm_split_kernel<2, 2, 4, 1, false, true>", 118784): ("matmul 1000 x 1800 x 700 (row strides 703 / 1805 / 1807)", 1),
+    ("gemm_split_kernel<2, 4, 4, 1, false, true>", 61440): ("matmul 1000 x 1800 x 700 (row strides 703 / 1805 / 1807)", 1),
     ("gemm_split_kernel<2, 2, 4, 0, true, false>", 65536): ("matmul 1024^3, B column-major", 1),
     ("softmax_rows_kernel<4, true>", 262144): ("softmax 4096 x 1024", 1),
     ("softmax_wg_kernel<2, 512, true>", 2097152): ("softmax 4096 x 4096", 1),

@@ -69,9 +69,39 @@ def test_linear_up_to_64_rows(M, N, K, relu):
     np.testing.assert_array_equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("K,kq", [(256, 4), (512, 8), (768, 0), (1024, 16), (1280, 0)])
+def test_linear_aligned_rows_whole_k_range_per_lane_group(K, kq):
+    """16-byte aligned rows and K % 256 == 0 take the vector-load kernel; at K = 256, 512 and
+    1024 (every decoder product) it is instantiated for that K and loads a lane group's whole
+    K range at once, other K loop over it. Either way: bias, ReLU and a residual that is the
+    output itself (read before it is written), padding untouched, the same bits twice, within
+    1e-6 of float64."""
+    M, N = 64, 272
+    rng = np.random.default_rng(K)
+    x = rng.standard_normal((M, K + 4)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    r = rng.standard_normal((M, N + 4)).astype(np.float32)
+    tx, tw, tb = (torch.from_numpy(t).cuda() for t in (x, w, b))
+    outs = []
+    for _ in range(2):
+        y = torch.from_numpy(r).cuda()  # the residual, updated in place
+        rt.linear(tx, K + 4, tw, tb, y, N + 4, y, N + 4, M, N, K, relu=True)
+        (launch,) = rt.last_launches()
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+        assert launch["kernel"] == f"gemm_small_m_kernel<true, false, {kq}>", launch
+        assert launch["grid"] == ((N + 15) // 16, (M + 15) // 16, 1) and launch["scratch_bytes"] == 0, launch
+    ref = np.maximum(x[:, :K].astype(np.float64) @ w + b, 0) + r[:, :N]
+    assert fp64.rel_fro(outs[0][:, :N], ref) <= 1e-6
+    np.testing.assert_array_equal(outs[0][:, N:], r[:, N:])
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("M,N,K,relu,ldx", [(64, 768, 256, False, 256), (64, 1024, 256, True, 260),
                                             (64, 256, 256, False, 256), (17, 100, 512, True, 516),
-                                            (1, 16, 256, False, 256)])
+                                            (1, 16, 256, False, 256), (32, 256, 1024, True, 1028),
+                                            (64, 64, 768, False, 768)])
 def test_layernorm_fused_linear_equals_the_two_launches(M, N, K, relu, ldx):
     """linear_ln = layernorm then linear, bit for bit (the decoder's decode steps fuse them),
     with bias, ReLU, a residual and strided rows; and within 1e-6 of float64."""

@@ -150,10 +150,12 @@ PITON_API int32_t piton_mi355x_linear(const float *x, int64_t ldx, const float *
 /* The digits MLP chain (examples/digits_model.py:120-139: three dense_layer_kernel launches of
  * examples/nn_kernels.py:23-74 with ReLU on the hidden layers, then numpy's argmax of the
  * first n_classes logits) in one launch: x [M, k0] row-major, w_l [K_l, N_l] row-major, biases
- * nullable. logits [M, n3] (nullable) are bit-identical to the three piton_mi355x_dense launches;
- * pred (nullable) gets the predictions. Layer sizes even and <= 256 (n3 <= 256, any parity),
- * else PITON_EUNSUPPORTED. No reference counterpart: one launch for the chain the reference
- * runs as three. */
+ * nullable; logits [M, n3] and pred (the predictions) nullable. The digits network (64 -> 128
+ * -> 64 -> 10 or 16, x 16-byte aligned) runs on 16-row tiles in another k order than the dense
+ * GEMM's: its logits are within the float32 error bound of the chain, not the dense launches'
+ * bits. Other sizes: logits bit-identical to the three piton_mi355x_dense launches. Layer sizes
+ * even and <= 256 (n3 <= 256, any parity), else PITON_EUNSUPPORTED. No reference counterpart:
+ * one launch for the chain the reference runs as three. */
 PITON_API int32_t piton_mi355x_mlp3(const float *x, int64_t M, const float *w1, const float *b1,
                           const float *w2, const float *b2, const float *w3, const float *b3,
                           int64_t k0, int64_t n1, int64_t n2, int64_t n3, float *logits,

@@ -53,8 +53,10 @@ class MLP:
     def run(self, x: torch.Tensor, fused: bool = True):
         """Logits [M, N_last] and predictions [M] (int32) for float32 x [M, 64] on the GPU;
         asynchronous on the current stream. A three-layer chain whose sizes fit (even, <= 256)
-        runs as one launch (`mlp3`, the same logits bit for bit); otherwise, or with
-        fused=False, as one dense launch per layer with the argmax fused into the last."""
+        runs as one launch (`mlp3`: for the digits network in another k order than the dense
+        GEMM, logits equal to the dense launches' within the chain's float32 error bound; for
+        other sizes bit for bit); otherwise, or with fused=False, as one dense launch per layer
+        with the argmax fused into the last."""
         M = x.shape[0]
         if M > self.max_batch:
             raise ValueError(f"batch {M} exceeds max_batch {self.max_batch}")

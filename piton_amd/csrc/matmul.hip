@@ -519,19 +519,20 @@ void gemm_direct_kernel(GemmArgs g) {
 }
 
 // Shapes with too few 128 x 128 tiles to fill the chip (config 2's 512^3 has 16 and 1024^3 64
-// for 256 CUs) or with ragged edges: a workgroup owns a TB x TB tile (TB = 32 NB) and
-// its KS waves split K, each wave computing the whole tile, NB x NB blocks of
-// v_mfma_f32_32x32x2_f32, over the K tiles kt = wave, wave + KS, ... (interleaved, so the waves
-// read neighbouring k together). Operands go from memory straight into registers as in the
-// direct kernel (the same k order inside a K tile of 32: lane half h supplies k = 16 h + s at
-// step s), through buffer descriptors bounded at each matrix's last element. The K tail (k >= K
-// inside the last tile, which may hold padding or the next row or column) reads as zeros, as the
-// reference's K mask makes it: a row-major A's elements there, and a column-major B's, take an
-// offset past the bound; a column-major A's (columns at least M floats apart) and a row-major
-// B's rows past K lie past the bound already. Rows of A past M and columns of B past N feed only
-// rows and columns of C that are not stored. The KS partial tiles meet in LDS and add in wave
-// order (fixed: the result does not depend on timing); the epilogue (bias, ReLU, residual) then
-// stores rows < M and columns < N.
+// for 256 CUs) or with ragged edges: a workgroup owns a 32 NB x 32 NBN tile and its KS waves
+// split K, each wave computing the whole tile, NB x NBN blocks of v_mfma_f32_32x32x2_f32, over
+// the K tiles kt = wave, wave + KS, ... (interleaved, so the waves read neighbouring k together).
+// Operands go from memory straight into registers as in the direct kernel (the same k order
+// inside a K tile of 32: lane half h supplies k = 16 h + s at step s), through buffer
+// descriptors bounded at each matrix's last element. The K tail (k >= K inside the last tile,
+// which may hold padding or the next row or column) reads as zeros, as the reference's K mask
+// makes it: a row-major A's values there are masked (16-byte chunks by their offset, an
+// unaligned row's values after its shift), a column-major B's chunks take an offset past the
+// bound; a column-major A's elements (columns at least M floats apart) and a row-major B's rows
+// past K (rows at least N floats apart) lie past the bound already. Rows of A past M and columns
+// of B past N feed only rows and columns of C that are not stored. The KS partial tiles meet in
+// LDS and add in wave order (fixed: the result does not depend on timing); the epilogue (bias,
+// ReLU, residual) then stores rows < M and columns < N.
 // AM: A's layout. A_ROW16: row-major, rows 16-byte aligned (16-byte loads along k). A_ROW:
 // row-major, each lane's 16 consecutive A values sit r = (row start) mod 4 floats past a 16-byte
 // boundary, the same r for every K tile: the lane loads the five aligned 16-byte chunks that
@@ -1118,12 +1119,14 @@ static SplitPlan plan_split(const GemmArgs &g, int cus) {
     SplitPlan p{0, 0, 0, A_ROW16, false, 0};
     if (g.K <= 0 || g.M <= 0 || g.N <= 0) return p;
     // A with stride 1 along K (16-byte loads where its rows are 16-byte aligned and K % 4 == 0) or
-    // along M with columns at least M floats apart; B with stride 1 along N, or along K with
-    // 16-byte aligned columns and K % 4 == 0
+    // along M with columns at least M floats apart; B with stride 1 along N and rows at least N
+    // floats apart, or with stride 1 along K, 16-byte aligned columns and K % 4 == 0
     if (g.s_ak == 1 && g.s_am > 0) p.am = g.s_am % 4 == 0 && g.K % 4 == 0 && aligned16(g.a) ? A_ROW16 : A_ROW;
     else if (g.s_am == 1 && g.s_ak >= g.M) p.am = A_COL;
     else return p;
-    if (g.s_bn == 1 && g.s_bk > 0) p.bkc = false;
+    // (a row-major B's rows no closer than N floats apart: then the rows past K of the last K
+    // tile lie past the descriptor's bound and read as zeros)
+    if (g.s_bn == 1 && g.s_bk >= g.N) p.bkc = false;
     else if (g.s_bk == 1 && g.s_bn > 0 && g.s_bn % 4 == 0 && g.K % 4 == 0 && aligned16(g.b)) p.bkc = true;
     else return p;
     auto tiles2 = [&](int64_t tm, int64_t tn) { return sat_mul((g.M + tm - 1) / tm, (g.N + tn - 1) / tn); };

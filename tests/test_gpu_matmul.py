@@ -480,6 +480,28 @@ def test_split_kernel_uniform_against_float64_and_oracle(M, N, K, pad_a, pad_b):
     assert fp64.rel_fro(got[rows], ref[rows]) <= fp64.rel_fro(emu, ref[rows])
 
 
+@pytest.mark.parametrize("ldb,split", [(64, False), (96, True)])
+def test_row_major_b_with_overlapping_rows(ldb, split):
+    """B row-major with rows closer together than N floats (a strided view whose rows overlap):
+    the split kernel relies on B's rows past K lying past the end of B for its K tail, which
+    overlapping rows break, so such a B takes the LDS kernel and its masks; rows N apart keep
+    the split kernel. Either way within the float32 bound of float64 over the view's values."""
+    M, N, K = 200, 96, 100  # K % 32 != 0: a partial last K tile
+    rng = np.random.default_rng(ldb)
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    store = rng.uniform(-1, 1, (K - 1) * ldb + N).astype(np.float32)
+    b = np.lib.stride_tricks.as_strided(store, (K, N), (4 * ldb, 4))
+    ref = fp64.matmul(a, np.ascontiguousarray(b))
+    bound = (K + 2) * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+    A, B = torch.from_numpy(a).cuda(), torch.from_numpy(store).cuda()
+    C = torch.full((M, N), -1.0, device="cuda")
+    rt.matmul(A, B, C, M, N, K, K, 1, ldb, 1, N, 1, 8)
+    (launch,) = rt.last_launches()
+    torch.cuda.synchronize()
+    assert launch["kernel"].startswith("gemm_split_kernel") == split, launch
+    assert not (np.abs(C.cpu().numpy() - ref) > bound).any()
+
+
 def test_split_kernel_group_order_and_repeatability():
     g = torch.Generator(device="cuda").manual_seed(21)
     a = torch.rand((1000, 700), device="cuda", generator=g)
